@@ -1,0 +1,337 @@
+"""Pins the CPU oracle (oracle/oracle.c) before anything is checked against it.
+
+Each oracle function is checked against something that does not restate its
+own formula: the reference's golden vectors (tests/golden/, copied from
+benchmarks/torch_ref/), the reference's own known-answer tests, published
+vectors, exact integer closed forms, or IEEE facts chosen so that a dropped
+term, a wrong index/sign or a transposed operand fails.
+
+Pin map (function -> checks in this file):
+  bf16_to_f32        exhaustive 65536 patterns vs torch's bfloat16 decode
+  bf16_rne           1M random patterns + ties/specials vs torch RNE cast
+  bf16_trunc         tests/tile_gemm_contract.rs:136-154 known answers
+  xorshift_bf16      Marsaglia's published xorshift64(13,7,17) states
+  gemm_nt / gemm_nn  torch_ref fixtures; integer closed forms (hello_gemm_gen
+                     all-ones, auto_gemm smoke pattern, tile_ir structured
+                     pattern); NN == NT on B^T; sequential-order IEEE case
+  gemm_rows          equals the full product's rows
+  splitk_sum         IEEE order case + integer planes
+  int4 pack/unpack   src/t0/quant_kernels.rs:347-491 known answers
+  dequant_int4_*     brute force over all (q, z) x scales vs exact product
+  w4a16              integer closed form; equals dequant + f64 bound
+  gptq bytes         src/t0/quant_kernels.rs:384-422 round trip, :480-490 size
+"""
+import os
+import struct
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+
+torch = pytest.importorskip("torch")
+
+
+def _load(golden_dir, name, dtype):
+    return np.fromfile(os.path.join(golden_dir, name), dtype=dtype)
+
+
+# ------------------------------------------------------------------ bf16 --
+
+def test_bf16_decode_exhaustive_vs_torch():
+    h = np.arange(65536, dtype=np.uint16)
+    ours = orc.bf16_to_f32(h)
+    theirs = torch.from_numpy(h.view(np.int16).copy()).view(torch.bfloat16).float().numpy()
+    assert np.array_equal(ours.view(np.uint32), theirs.view(np.uint32))
+
+
+def test_bf16_rne_matches_torch_cast():
+    rng = np.random.default_rng(7)
+    bits = rng.integers(0, 2**32, size=1_000_000, dtype=np.uint64).astype(np.uint32)
+    # add exact ties (low half == 0x8000) with both parities, and specials
+    ties = (rng.integers(0, 2**16, size=4096, dtype=np.uint32) << 16) | 0x8000
+    specials = np.array([0, 0x80000000, 0x7F800000, 0xFF800000, 0x7F7FFFFF,
+                         0x3F808000, 0x3F818000, 0x00000001, 0x807FFFFF], dtype=np.uint32)
+    bits = np.concatenate([bits, ties, specials])
+    x = bits.view(np.float32)
+    finite = np.isfinite(x) | np.isinf(x)
+    x = x[finite]
+    ours = orc.bf16_rne(x)
+    theirs = torch.from_numpy(x.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(ours, theirs)
+
+
+def test_bf16_rne_nan_is_quiet_nan():
+    for b in (0x7F800001, 0x7FC00000, 0xFFFFFFFF, 0x7FFFFFFF):
+        h = orc.lib().orc_bf16_rne(np.uint32(b).view(np.float32).item())
+        assert (h & 0x7F80) == 0x7F80 and (h & 0x007F) != 0
+
+
+def test_bf16_rne_known_answers():
+    # reference RNE formula (test_gemm_correctness.rs:15-20) on hand-worked cases
+    f = orc.lib().orc_bf16_rne
+    assert f(1.0) == 0x3F80
+    assert f(-1.0) == 0xBF80
+    assert f(np.uint32(0x3F808000).view(np.float32).item()) == 0x3F80   # tie -> even
+    assert f(np.uint32(0x3F818000).view(np.float32).item()) == 0x3F82   # tie -> even (up)
+    assert f(np.uint32(0x3F808001).view(np.float32).item()) == 0x3F81   # above tie
+
+
+def test_bf16_trunc_contract():
+    """tests/tile_gemm_contract.rs:136-154 (f32_to_bf16_truncation_semantics)."""
+    f = orc.lib().orc_bf16_trunc
+    assert f(1.0) == 0x3F80
+    assert f(-1.0) == 0xBF80
+    assert f(0.0) == 0
+    assert f(float("inf")) == 0x7F80
+    assert f(float("-inf")) == 0xFF80
+    slightly_over = np.uint32(0x3F800000 + 0x00FF).view(np.float32).item()
+    assert f(slightly_over) == 0x3F80
+    nan = np.float32(np.nan)
+    assert f(float(nan)) == (int(nan.view(np.uint32)) >> 16)
+    for bits in (0x3F80, 0xBF80, 0x007F, 0x8000):
+        assert f(float(orc.bf16_to_f32(np.array([bits], dtype=np.uint16))[0])) == bits
+
+
+# ------------------------------------------------------------- xorshift --
+
+def test_xorshift_matches_published_states():
+    """Marsaglia (2003) xor64 with x=88172645463325252 yields the states
+    8748534153485358512, 3040900993826735515, 3453997556048239312.  The
+    reference maps each state s to bf16_rne((s>>32)/2^32 * 2 - 1)."""
+    published = [8748534153485358512, 3040900993826735515, 3453997556048239312]
+    seed = 88172645463325252 ^ 0xDEADBEEFCAFEBABE
+    got = orc.xorshift_bf16(3, seed)
+    for s, g in zip(published, got):
+        q = np.float32(s >> 32) / np.float32(4294967296.0)
+        f = q * np.float32(2.0) - np.float32(1.0)
+        want = torch.tensor([float(f)], dtype=torch.float32).to(torch.bfloat16).view(torch.int16).item() & 0xFFFF
+        assert g == want
+    big = orc.bf16_to_f32(orc.xorshift_bf16(100_000, 1234))
+    assert big.min() >= -1.0 and big.max() <= 1.0
+    assert abs(float(big.mean())) < 0.02
+
+
+# ----------------------------------------------------------------- GEMM --
+
+def test_gemm_nt_torch_fixture_h_gate(golden_dir):
+    """benchmarks/torch_ref: h_gate_f32ref = X.float() @ W_gate.float().T (M=64,K=256,N=512)."""
+    x = _load(golden_dir, "x.bin", np.uint16).reshape(64, 256)
+    w = _load(golden_dir, "w_gate.bin", np.uint16).reshape(512, 256)
+    ref = _load(golden_dir, "h_gate_f32ref.bin", np.float32).reshape(64, 512)
+    y = orc.gemm_nt(x, w)
+    # torch sums in another order; both are within f32 rounding of the exact sum
+    exact = orc.gemm_f64(x, w, "nt")
+    bound = 256 * 2.0**-24 * np.abs(orc.bf16_to_f32(x)).astype(np.float64) @ np.abs(orc.bf16_to_f32(w)).T
+    assert np.all(np.abs(y - exact) <= bound + 1e-30)
+    assert np.all(np.abs(ref - exact) <= bound + 1e-30)
+    assert np.max(np.abs(y - ref)) < 2e-6
+
+
+def test_gemm_nt_torch_fixture_bf16_output(golden_dir):
+    """h_gate_bf16acc is torch's bf16 mm (bf16 output).  RNE of the oracle's
+    f32 result must agree except on a handful of near-ties."""
+    x = _load(golden_dir, "x.bin", np.uint16).reshape(64, 256)
+    w = _load(golden_dir, "w_gate.bin", np.uint16).reshape(512, 256)
+    ref = _load(golden_dir, "h_gate_bf16acc.bin", np.float32).reshape(64, 512)
+    ours = orc.bf16_to_f32(orc.bf16_rne(orc.gemm_nt(x, w)))
+    eq = np.mean(ours == ref)
+    assert eq > 0.999
+    # any disagreement is one bf16 ulp
+    ulp = np.abs(ref) * 2.0**-7
+    assert np.all(np.abs(ours - ref) <= ulp + 1e-30)
+
+
+def test_gemm_nt_torch_fixture_second_gemm(golden_dir):
+    """y_bf16_f32acc = swiglu_bf16_trunc.float() @ W_down.float().T (M=64,K=512,N=256)."""
+    s = _load(golden_dir, "swiglu_bf16_trunc.bin", np.uint16).reshape(64, 512)
+    wd = _load(golden_dir, "w_down.bin", np.uint16).reshape(256, 512)
+    ref = _load(golden_dir, "y_bf16_f32acc.bin", np.float32).reshape(64, 256)
+    y = orc.gemm_nt(s, wd)
+    exact = orc.gemm_f64(s, wd, "nt")
+    bound = 512 * 2.0**-24 * np.abs(orc.bf16_to_f32(s)).astype(np.float64) @ np.abs(orc.bf16_to_f32(wd)).T
+    assert np.all(np.abs(y - exact) <= bound + 1e-30)
+    assert np.max(np.abs(y - ref)) < 1e-5
+
+
+def _bf16_of_ints(v):
+    return orc.bf16_rne(np.asarray(v, dtype=np.float32))
+
+
+def test_gemm_all_ones_is_k():
+    """examples/hello_gemm_gen.rs:143-146: all-ones inputs give exactly K."""
+    m, k, n = 33, 300, 17
+    a = _bf16_of_ints(np.ones((m, k)))
+    b = _bf16_of_ints(np.ones((n, k)))
+    assert np.all(orc.gemm_nt(a, b) == k)
+
+
+@pytest.mark.parametrize("layout", ["nt", "nn"])
+def test_gemm_integer_patterns_exact(layout):
+    """Smoke pattern of src/t0/auto_gemm.rs:235-238 and the structured pattern
+    of src/t0/tile_ir.rs:5056-5057: small integers, so every partial sum is
+    exact in f32 and the result must equal the int64 product."""
+    for (m, k, n, fa, fb) in [(256, 256, 256, lambda i: i % 7 - 3, lambda j: j % 5 - 2),
+                              (64, 160, 96, lambda i: i % 17 - 8, lambda j: j % 13 - 6)]:
+        ai = fa(np.arange(m * k)).reshape(m, k)
+        bi_nt = fb(np.arange(n * k)).reshape(n, k)
+        a = _bf16_of_ints(ai)
+        if layout == "nt":
+            y = orc.gemm_nt(a, _bf16_of_ints(bi_nt))
+        else:
+            y = orc.gemm_nn(a, _bf16_of_ints(bi_nt.T.copy()))
+        want = ai.astype(np.int64) @ bi_nt.T.astype(np.int64)
+        assert np.array_equal(y.astype(np.int64), want)
+
+
+def test_gemm_nn_equals_nt_on_transpose():
+    rng = np.random.default_rng(3)
+    a = orc.bf16_rne(rng.standard_normal((40, 72)).astype(np.float32))
+    b = orc.bf16_rne(rng.standard_normal((72, 56)).astype(np.float32))
+    assert np.array_equal(orc.gemm_nn(a, b).view(np.uint32),
+                          orc.gemm_nt(a, b.T.copy()).view(np.uint32))
+
+
+def test_gemm_sequential_order():
+    """acc starts at 0 and adds a_k*b_k in increasing k: with terms
+    [1, 2^27, -2^27] the 1 is absorbed (2^27+1 rounds to 2^27) and the result
+    is 0; any other association (e.g. pairwise) returns 1."""
+    a = _bf16_of_ints([[1.0, 2.0**27, -(2.0**27)]])
+    b = _bf16_of_ints([[1.0, 1.0, 1.0]])
+    assert orc.gemm_nt(a, b)[0, 0] == 0.0
+    a2 = _bf16_of_ints([[2.0**27, -(2.0**27), 1.0]])
+    assert orc.gemm_nt(a2, b)[0, 0] == 1.0
+
+
+def test_gemm_rows_slice():
+    rng = np.random.default_rng(5)
+    a = orc.bf16_rne(rng.standard_normal((48, 64)).astype(np.float32))
+    b = orc.bf16_rne(rng.standard_normal((64, 40)).astype(np.float32))
+    full = orc.gemm_nn(a, b)
+    assert np.array_equal(orc.gemm_rows(a, b, "nn", 16, 32), full[16:32])
+    assert np.array_equal(orc.gemm_rows(a, b.T.copy(), "nt", 0, 8), full[0:8])
+
+
+def test_splitk_sum():
+    planes = np.zeros((3, 2, 2), dtype=np.float32)
+    planes[:, 0, 0] = [1.0, 2.0**27, -(2.0**27)]       # sequential: 0
+    planes[:, 1, 1] = [3.0, 4.0, 5.0]
+    y = orc.splitk_sum(planes)
+    assert y[0, 0] == 0.0 and y[1, 1] == 12.0 and y[0, 1] == 0.0
+
+
+# ----------------------------------------------------------------- INT4 --
+
+def test_int4_known_answers():
+    """src/t0/quant_kernels.rs: :350-357 (0xAB), :457-466 (0xD7 -> -1, 5),
+    :381-389 (pack 3|7<<4), :365-372 ((12-8)*0.5 = 2.0), :469-479 (group idx)."""
+    L = orc.lib()
+    ab = np.array([0xAB], dtype=np.uint8)
+    assert L.orc_int4_get(ab.ctypes.data, 0) == 11
+    assert L.orc_int4_get(ab.ctypes.data, 1) == 10
+    d7 = np.array([0xD7], dtype=np.uint8)
+    lo, hi = L.orc_int4_get(d7.ctypes.data, 0), L.orc_int4_get(d7.ctypes.data, 1)
+    assert (lo, hi) == (7, 13)
+    assert (int(lo) - 8, int(hi) - 8) == (-1, 5)
+    assert orc.int4_pack(np.array([3, 7]))[0] == 0x73
+    # (12 - 8) * 0.5 through the dequant path
+    packed = orc.int4_pack(np.array([12, 0], dtype=np.uint8))
+    out = orc.dequant_int4_f32(packed, np.array([0.5], np.float32), np.array([8], np.int32), 1, 2, 2)
+    assert out[0, 0] == 2.0 and out[0, 1] == -4.0
+    # group index: element 200 of a 256-wide row with gs=128 uses group 1
+    q = np.zeros(256, np.uint8)
+    q[200] = 9
+    q[127] = 9
+    out = orc.dequant_int4_f32(orc.int4_pack(q), np.array([1.0, 2.0], np.float32),
+                               np.array([0, 0], np.int32), 1, 256, 128)
+    assert out[0, 200] == 18.0 and out[0, 127] == 9.0
+
+
+def test_int4_pack_roundtrip():
+    rng = np.random.default_rng(11)
+    q = rng.integers(0, 16, size=4096, dtype=np.uint8)
+    p = orc.int4_pack(q)
+    assert np.array_equal(orc.int4_unpack(p, q.size), q)
+    # viewed as little-endian u32: 8 nibbles per word, nibble i at bits 4i
+    w = p.view("<u4")
+    for i in range(8):
+        assert np.array_equal((w >> (4 * i)) & 0xF, q[i::8])
+
+
+def test_dequant_bruteforce_exact():
+    """Every (q, z) pair with a spread of bf16 scales: (q - z) * s is exact in
+    f32, so the oracle must equal the exact product bit for bit."""
+    scales_bf16 = np.array([0x3F80, 0x3C23, 0x3BA4, 0x3CA3, 0x4120, 0x0080, 0x7F7F, 0xBF40,
+                            0x3D4D, 0x3E2B], dtype=np.uint16)
+    scales = orc.bf16_to_f32(scales_bf16)
+    rows, cols, gs = 16 * len(scales), 16, 16      # one group per row
+    q = np.tile(np.arange(16, dtype=np.uint8), rows)
+    zp = np.repeat(np.arange(16, dtype=np.int32), len(scales))
+    sc = np.tile(scales, 16)
+    out = orc.dequant_int4_f32(orc.int4_pack(q), sc, zp, rows, cols, gs)
+    for r in range(rows):
+        exact = (np.arange(16, dtype=np.float64) - zp[r]) * np.float64(sc[r])
+        # exact in f32 unless it overflows, where IEEE rounding gives +-inf
+        with np.errstate(over="ignore"):
+            assert np.array_equal(out[r], exact.astype(np.float32)), r
+    outb = orc.dequant_int4_bf16(orc.int4_pack(q), sc, zp, rows, cols, gs)
+    assert np.array_equal(outb, (out.view(np.uint32) >> 16).astype(np.uint16))
+
+
+def test_w4a16_integer_closed_form():
+    """Scales 1.0, z = 8: weights are q - 8 exactly; with integer activations
+    the f32 sum is exact and must equal the int64 product."""
+    rng = np.random.default_rng(2)
+    m, n, k, gs = 5, 24, 256, 128
+    q = rng.integers(0, 16, size=(n, k), dtype=np.uint8)
+    qw = orc.int4_pack(q.reshape(-1)).view("<u4").reshape(n, k // 8)
+    ai = rng.integers(-4, 5, size=(m, k))
+    a = _bf16_of_ints(ai)
+    scales = np.full((n, k // gs), 0x3F80, np.uint16)
+    y = orc.w4a16(a, qw, scales, None, 8, m, n, k, gs)
+    want = ai.astype(np.int64) @ (q.astype(np.int64) - 8).T
+    assert np.array_equal(y.astype(np.int64), want)
+
+
+def test_w4a16_per_group_zeros_and_scales():
+    rng = np.random.default_rng(4)
+    m, n, k, gs = 3, 16, 512, 128
+    G = k // gs
+    q = rng.integers(0, 16, size=(n, k), dtype=np.uint8)
+    qw = orc.int4_pack(q.reshape(-1)).view("<u4").reshape(n, k // 8)
+    z = rng.integers(0, 16, size=(n, G), dtype=np.uint8)
+    zw = np.zeros((n, (G + 7) // 8), np.uint32)
+    for g in range(G):
+        zw[:, g // 8] |= z[:, g].astype(np.uint32) << (4 * (g % 8))
+    s = orc.bf16_rne(rng.uniform(0.005, 0.02, size=(n, G)).astype(np.float32))
+    a = orc.bf16_rne(rng.standard_normal((m, k)).astype(np.float32))
+    w = orc.w4a16_dequant(qw, s, zw, 0, n, k, gs)
+    # dequant equals the GPTQ-format dequant on the same data
+    packed = orc.int4_pack(q.reshape(-1))
+    w2 = orc.dequant_int4_f32(packed, orc.bf16_to_f32(s).reshape(-1), z.astype(np.int32).reshape(-1), n, k, gs)
+    assert np.array_equal(w.view(np.uint32), w2.view(np.uint32))
+    y = orc.w4a16(a, qw, s, zw, 0, m, n, k, gs)
+    exact = orc.bf16_to_f32(a).astype(np.float64) @ w.astype(np.float64).T
+    bound = k * 2.0**-24 * (np.abs(orc.bf16_to_f32(a)).astype(np.float64) @ np.abs(w).astype(np.float64).T)
+    assert np.all(np.abs(y - exact) <= bound + 1e-30)
+    # rows slice
+    assert np.array_equal(orc.w4a16(a, qw, s, zw, 0, m, n, k, gs, 1, 3), y[1:3])
+
+
+# ----------------------------------------------------------- GPTQ bytes --
+
+def test_gptq_from_bytes_roundtrip():
+    """src/t0/quant_kernels.rs:384-422: 16x16, gs=16, packed 0xAB, scales 1.0, zp 8."""
+    raw = struct.pack("<III", 16, 16, 16) + bytes([0xAB]) * 128 \
+        + struct.pack("<16f", *([1.0] * 16)) + struct.pack("<16i", *([8] * 16))
+    rows, cols, gs, ng, packed, scales, zps = orc.gptq_from_bytes(raw)
+    assert (rows, cols, gs, ng) == (16, 16, 16, 1)
+    assert packed.size == 128 and scales.size == 16 and zps.size == 16
+    assert np.all(scales == 1.0) and np.all(zps == 8)
+    assert orc.gptq_to_bytes(rows, cols, gs, packed, scales, zps) == raw
+    # gpu_buffer_size (:480-490): 128 + 16*4 + 16*4 = 256
+    assert packed.size + scales.size * 4 + zps.size * 4 == 256
+    with pytest.raises(ValueError):
+        orc.gptq_from_bytes(raw[:11])
+    with pytest.raises(ValueError):
+        orc.gptq_from_bytes(raw[:-1])
