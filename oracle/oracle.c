@@ -232,28 +232,36 @@ void orc_dequant_int4_bf16(const uint8_t* packed, const float* scales,
 
 /* Weight W for output column n is row n of the GPTQ packed matrix
  * [rows=N][cols=K] (quant_kernels.rs:191-199), i.e. qw[n*(K/8) + k/8] as a
- * little-endian u32 holds k at bits 4*(k%8).  Scales are bf16 [N][K/gs];
- * zero points are either the constant zc (zeros == NULL) or packed 4-bit
- * [N][G/8] words, group g at bits 4*(g%8) of word n*(G/8) + g/8.
+ * little-endian u32 holds k at bits 4*(k%8).  Scales are bf16 [G][N]
+ * (G = K/gs, n contiguous); zero points are either the constant zc
+ * (zeros == NULL) or packed 4-bit [G][N/8] words, column n of group g at bits
+ * 4*(n%8) of word g*(N/8) + n/8 (the GPTQ qzeros packing).
  *
  * y[i,n] = sum_k bf16(a[i,k]) * w(n,k) with w = (q - z) * s in f32 (exact:
  * |q - z| <= 15 and s has 8 significant bits), accumulated in f32 in k order
  * without FMA -- the reference CPU loop (examples/test_gemm_correctness.rs:28-42)
  * applied to the dequantized weights (src/t0/quant_kernels.rs:365-372). */
+static inline float w4_weight(const uint32_t* qw, const uint16_t* scales,
+                              const uint32_t* zeros, uint32_t zc,
+                              size_t j, size_t kk, size_t n, size_t k, size_t gs)
+{
+    size_t kw = k / 8, nw = n / 8;
+    uint32_t q = (qw[j * kw + kk / 8] >> (4 * (kk % 8))) & 0xF;
+    size_t g = kk / gs;
+    uint32_t z = zeros ? ((zeros[g * nw + j / 8] >> (4 * (j % 8))) & 0xF) : zc;
+    float s = orc_bf16_to_f32(scales[g * n + j]);
+    return (float)((int32_t)q - (int32_t)z) * s;
+}
+
 void orc_w4a16_rows(const uint16_t* a, const uint32_t* qw, const uint16_t* scales,
                     const uint32_t* zeros, uint32_t zc, float* y,
                     size_t row0, size_t row1, size_t n, size_t k, size_t gs)
 {
-    size_t kw = k / 8, G = k / gs, gw = (G + 7) / 8;
     for (size_t i = row0; i < row1; i++)
         for (size_t j = 0; j < n; j++) {
             float acc = 0.0f;
             for (size_t kk = 0; kk < k; kk++) {
-                uint32_t q = (qw[j * kw + kk / 8] >> (4 * (kk % 8))) & 0xF;
-                size_t g = kk / gs;
-                uint32_t z = zeros ? ((zeros[j * gw + g / 8] >> (4 * (g % 8))) & 0xF) : zc;
-                float s = orc_bf16_to_f32(scales[j * G + g]);
-                float w = (float)((int32_t)q - (int32_t)z) * s;
+                float w = w4_weight(qw, scales, zeros, zc, j, kk, n, k, gs);
                 float p = orc_bf16_to_f32(a[i * k + kk]) * w;
                 acc = acc + p;
             }
@@ -273,12 +281,7 @@ void orc_w4a16_dequant(const uint32_t* qw, const uint16_t* scales,
                        const uint32_t* zeros, uint32_t zc, float* w,
                        size_t n, size_t k, size_t gs)
 {
-    size_t kw = k / 8, G = k / gs, gw = (G + 7) / 8;
     for (size_t j = 0; j < n; j++)
-        for (size_t kk = 0; kk < k; kk++) {
-            uint32_t q = (qw[j * kw + kk / 8] >> (4 * (kk % 8))) & 0xF;
-            size_t g = kk / gs;
-            uint32_t z = zeros ? ((zeros[j * gw + g / 8] >> (4 * (g % 8))) & 0xF) : zc;
-            w[j * k + kk] = (float)((int32_t)q - (int32_t)z) * orc_bf16_to_f32(scales[j * G + g]);
-        }
+        for (size_t kk = 0; kk < k; kk++)
+            w[j * k + kk] = w4_weight(qw, scales, zeros, zc, j, kk, n, k, gs);
 }

@@ -1,0 +1,1138 @@
+// runtime.cpp -- HIP runtime side of libt0gpu: device/stream, code-object
+// loading, kernarg decoding and dispatch, buffers, events, the high-level GEMM
+// and W4A16 entry points and the measured tuner.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <map>
+#include <mutex>
+#include <sstream>
+#include <string>
+#include <sys/stat.h>
+#include <vector>
+
+#include "internal.hpp"
+
+using namespace t0h;
+
+// The gfx950 code object with every kernel of the library (embed.S).
+extern "C" const unsigned char t0_hsaco_start[];
+extern "C" const unsigned char t0_hsaco_end[];
+
+enum KernelKind { KK_RAW = 0, KK_GEMM_GEN = 1, KK_TILE = 2 };
+
+struct t0_kernel {
+    KernelKind kind = KK_RAW;
+    hipFunction_t fn = nullptr;
+    hipModule_t own_module = nullptr;   // RAW kernels loaded from a caller's code object
+    uint32_t wg[3] = {64, 1, 1};
+    uint32_t lds = 0;
+    uint32_t kernarg_size = 0;
+    std::string name;
+    const GemmInstance* inst = nullptr;
+    t0_gemm_config cfg{};
+    t0_tile_gemm tile{};
+    TileArgLayout layout;
+};
+
+struct t0_buffer {
+    struct t0_runtime* rt = nullptr;
+    void* ptr = nullptr;
+    size_t size = 0, alloc_size = 0;
+};
+
+struct t0_event {
+    hipEvent_t ev = nullptr;
+};
+
+struct t0_runtime {
+    int device = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    hipModule_t module = nullptr;
+    std::mutex mu;
+    std::map<std::string, t0_kernel*> cache;
+    std::map<std::string, hipFunction_t> fns;
+    std::atomic<bool> poisoned{false};
+    std::map<size_t, std::vector<t0_buffer*>> pool;
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    uint32_t* sem = nullptr;
+    size_t sem_count = 0;
+    uint32_t slot = 0;
+    std::string arch;
+    int cu_count = 0, clock_khz = 0;
+};
+
+#define HIPCHK(expr)                                                                          \
+    do {                                                                                      \
+        hipError_t e_ = (expr);                                                               \
+        if (e_ != hipSuccess) return fail(T0_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+namespace {
+
+int set_dev(t0_runtime* rt) {
+    HIPCHK(hipSetDevice(rt->device));
+    return T0_OK;
+}
+
+int get_fn(t0_runtime* rt, const std::string& sym, hipFunction_t* out) {
+    auto it = rt->fns.find(sym);
+    if (it != rt->fns.end()) { *out = it->second; return T0_OK; }
+    hipFunction_t f;
+    hipError_t e = hipModuleGetFunction(&f, rt->module, sym.c_str());
+    if (e != hipSuccess) return fail(T0_ERR_NOT_FOUND, "kernel %s not in code object: %s", sym.c_str(), hipGetErrorString(e));
+    rt->fns[sym] = f;
+    *out = f;
+    return T0_OK;
+}
+
+template <class P>
+int launch(t0_runtime* rt, hipFunction_t f, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t threads, const P& p) {
+    if (rt->poisoned.load()) return fail(T0_ERR_POISONED, "runtime poisoned after an earlier GPU failure; refusing dispatch");
+    if (gx == 0 || gy == 0 || gz == 0) return T0_OK;
+    P copy = p;
+    void* args[] = {&copy};
+    HIPCHK(hipModuleLaunchKernel(f, gx, gy, gz, threads, 1, 1, 0, rt->stream, args, nullptr));
+    return T0_OK;
+}
+
+int ensure_ws(t0_runtime* rt, size_t bytes) {
+    if (bytes <= rt->ws_bytes) return T0_OK;
+    if (rt->ws) { HIPCHK(hipStreamSynchronize(rt->stream)); HIPCHK(hipFree(rt->ws)); rt->ws = nullptr; rt->ws_bytes = 0; }
+    size_t want = std::max<size_t>(bytes + 4096, 64u << 20);
+    HIPCHK(hipMalloc(&rt->ws, want));
+    rt->ws_bytes = want;
+    return T0_OK;
+}
+
+int ensure_sem(t0_runtime* rt, size_t count) {
+    if (count <= rt->sem_count) return T0_OK;
+    if (rt->sem) { HIPCHK(hipStreamSynchronize(rt->stream)); HIPCHK(hipFree(rt->sem)); rt->sem = nullptr; rt->sem_count = 0; }
+    size_t want = std::max<size_t>(count, 65536);
+    HIPCHK(hipMalloc(&rt->sem, want * 4));
+    HIPCHK(hipMemsetAsync(rt->sem, 0, want * 4, rt->stream));
+    HIPCHK(hipStreamSynchronize(rt->stream));
+    rt->sem_count = want;
+    return T0_OK;
+}
+
+bool aligned16(uint64_t p) { return (p & 15) == 0; }
+
+// Fast tiled kernels need 16-byte rows; anything else takes the generic kernel.
+bool fast_ok(const t0_gemm_params& p, bool nn, bool out_bf16) {
+    if (!aligned16((uint64_t)p.A) || !aligned16((uint64_t)p.B) || !aligned16((uint64_t)p.C)) return false;
+    if (p.lda % 8 || p.ldb % 8 || p.ldc % 4) return false;
+    if (p.K % (8 * p.split_k)) return false;
+    if (nn && p.N % 8) return false;
+    (void)out_bf16;
+    return true;
+}
+
+int run_gemm_params(t0_runtime* rt, const GemmInstance* g, bool nn, t0_gemm_params& p, uint32_t threads_override = 0) {
+    const bool out_bf16 = p.flags & T0_GEMM_OUT_BF16;
+    hipFunction_t f;
+    if (!g || !fast_ok(p, nn, out_bf16)) {
+        if (p.flags & T0_GEMM_FIXUP) {   // generic kernel writes planes; reduce separately
+            return fail(T0_ERR_INVALID, "in-kernel split-K needs the tiled path (16-byte aligned rows)");
+        }
+        int r = get_fn(rt, nn ? "t0k_gemm_generic_nn" : "t0k_gemm_generic_nt", &f);
+        if (r) return r;
+        const uint32_t tiles = ((p.M + 63) / 64) * ((p.N + 63) / 64) * p.split_k;
+        return launch(rt, f, tiles, 1, 1, 256, p);
+    }
+    int r = get_fn(rt, g->symbol(nn), &f);
+    if (r) return r;
+    const uint32_t tiles = ((p.M + g->bm - 1) / g->bm) * ((p.N + g->bn - 1) / g->bn);
+    if (p.flags & T0_GEMM_FIXUP) {
+        r = ensure_ws(rt, (size_t)p.split_k * tiles * g->bm * g->bn * 4);
+        if (r) return r;
+        r = ensure_sem(rt, tiles);
+        if (r) return r;
+        p.workspace = (float*)rt->ws;
+        p.semaphores = rt->sem;
+    }
+    // grid x = tiles, y = split (the kernel linearises and remaps to XCDs)
+    return launch(rt, f, tiles, p.split_k, 1, threads_override ? threads_override : g->threads(), p);
+}
+
+uint32_t epi_ops_from_gemm_gen(uint8_t epi) {
+    if (epi == T0_EPI_BIAS_ADD) return T0_EPI_BIAS;
+    if (epi == T0_EPI_BIAS_ADD_RELU) return T0_EPI_BIAS | (T0_EPI_RELU << 4);
+    return 0;
+}
+
+uint64_t rd64(const uint8_t* p) { uint64_t v; memcpy(&v, p, 8); return v; }
+uint32_t rd32(const uint8_t* p) { uint32_t v; memcpy(&v, p, 4); return v; }
+float rdf(const uint8_t* p) { float v; memcpy(&v, p, 4); return v; }
+
+// ---------------------------------------------------------------- tuner --
+struct TunerState {
+    std::mutex mu;
+    std::map<std::string, std::pair<t0_gemm_config, double>> mem;
+    std::string dir;
+    uint32_t max_candidates = 8, n_iters = 10;
+};
+TunerState& tuner() {
+    static TunerState s;
+    return s;
+}
+
+std::string cache_dir() {
+    auto& T = tuner();
+    if (!T.dir.empty()) return T.dir;
+    if (const char* e = getenv("T0_AUTOTUNE_DIR")) return e;
+    const char* home = getenv("HOME");
+    return std::string(home ? home : "/tmp") + "/.t0_autotune";   // src/t0/auto_gemm.rs:594-600
+}
+
+std::string tune_key(const t0_runtime* rt, uint32_t m, uint32_t n, uint32_t k, uint32_t tr, uint32_t od) {
+    char b[160];
+    snprintf(b, sizeof b, "%s_%ux%ux%u_%s_%s", rt->arch.c_str(), m, n, k, tr == T0_NN ? "nn" : "nt",
+             od == T0_OUT_BF16 ? "bf16" : "f32");
+    return b;
+}
+
+bool load_cache(const std::string& key, t0_gemm_config* cfg, double* tf) {
+    std::ifstream f(cache_dir() + "/gemm_" + key + ".json");
+    if (!f) return false;
+    std::stringstream ss;
+    ss << f.rdbuf();
+    const std::string s = ss.str();
+    auto field = [&](const char* name) -> std::string {
+        std::string pat = std::string("\"") + name + "\":";
+        size_t p = s.find(pat);
+        if (p == std::string::npos) return "";
+        p += pat.size();
+        while (p < s.size() && (s[p] == ' ' || s[p] == '"')) p++;
+        size_t e = p;
+        while (e < s.size() && s[e] != '"' && s[e] != ',' && s[e] != '}') e++;
+        return s.substr(p, e - p);
+    };
+    if (field("version") != "1") return false;
+    const std::string name = field("name");
+    if (name.empty() || t0_config_from_name(name.c_str(), cfg) != T0_OK) return false;
+    *tf = atof(field("tflops").c_str());
+    return t0_config_is_feasible(cfg) || (cfg->split_k > 1);
+}
+
+void save_cache(const std::string& key, const t0_gemm_config& cfg, double tf) {
+    const std::string d = cache_dir();
+    mkdir(d.c_str(), 0755);
+    std::ofstream f(d + "/gemm_" + key + ".json");
+    if (!f) return;
+    f << "{\"version\": \"1\", \"key\": \"" << key << "\", \"name\": \"" << config_name(cfg) << "\", \"tflops\": "
+      << tf << "}\n";
+}
+
+}  // namespace
+
+// ================================================================= C ABI ==
+extern "C" {
+
+int t0_runtime_create(int device_ordinal, t0_runtime** out) {
+    if (!out) return fail(T0_ERR_INVALID, "null output");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return fail(T0_ERR_NO_DEVICE, "no HIP device visible");
+    if (device_ordinal < 0 || device_ordinal >= n) return fail(T0_ERR_NO_DEVICE, "device %d of %d", device_ordinal, n);
+    HIPCHK(hipSetDevice(device_ordinal));
+    hipDeviceProp_t prop;
+    HIPCHK(hipGetDeviceProperties(&prop, device_ordinal));
+    const std::string arch = prop.gcnArchName;
+    if (arch.compare(0, 6, "gfx950") != 0)
+        return fail(T0_ERR_NO_DEVICE, "device %d is %s; this library is built for gfx950 only", device_ordinal, arch.c_str());
+    auto* rt = new t0_runtime();
+    rt->device = device_ordinal;
+    rt->arch = "gfx950";
+    rt->cu_count = prop.multiProcessorCount;
+    rt->clock_khz = prop.clockRate;
+    hipError_t e = hipStreamCreateWithFlags(&rt->own_stream, hipStreamNonBlocking);
+    if (e != hipSuccess) { delete rt; return fail(T0_ERR_HIP, "hipStreamCreate: %s", hipGetErrorString(e)); }
+    rt->stream = rt->own_stream;
+    e = hipModuleLoadData(&rt->module, t0_hsaco_start);
+    if (e != hipSuccess) {
+        hipStreamDestroy(rt->own_stream);
+        delete rt;
+        return fail(T0_ERR_HIP, "hipModuleLoadData(embedded gfx950 code object): %s", hipGetErrorString(e));
+    }
+    *out = rt;
+    return T0_OK;
+}
+
+int t0_runtime_destroy(t0_runtime* rt) {
+    if (!rt) return T0_OK;
+    hipSetDevice(rt->device);
+    hipStreamSynchronize(rt->stream);
+    for (auto& kv : rt->cache) {
+        if (kv.second->own_module) hipModuleUnload(kv.second->own_module);
+        delete kv.second;
+    }
+    for (auto& kv : rt->pool)
+        for (auto* b : kv.second) { hipFree(b->ptr); delete b; }
+    if (rt->ws) hipFree(rt->ws);
+    if (rt->sem) hipFree(rt->sem);
+    if (rt->module) hipModuleUnload(rt->module);
+    if (rt->own_stream) hipStreamDestroy(rt->own_stream);
+    delete rt;
+    return T0_OK;
+}
+
+int t0_runtime_set_stream(t0_runtime* rt, void* s) {
+    if (!rt) return fail(T0_ERR_INVALID, "null runtime");
+    rt->stream = s ? (hipStream_t)s : rt->own_stream;
+    return T0_OK;
+}
+void* t0_runtime_stream(t0_runtime* rt) { return rt ? (void*)rt->stream : nullptr; }
+int t0_runtime_is_poisoned(const t0_runtime* rt) { return rt && rt->poisoned.load() ? 1 : 0; }
+int t0_runtime_mark_poisoned(t0_runtime* rt) {
+    if (!rt) return fail(T0_ERR_INVALID, "null runtime");
+    rt->poisoned.store(true);
+    fprintf(stderr, "[t0] runtime POISONED -- all subsequent dispatches fail fast\n");
+    return T0_OK;
+}
+
+int t0_runtime_device_info(const t0_runtime* rt, char* arch, size_t arch_len, int* cu, int* clk) {
+    if (!rt) return fail(T0_ERR_INVALID, "null runtime");
+    if (arch && arch_len) snprintf(arch, arch_len, "%s", rt->arch.c_str());
+    if (cu) *cu = rt->cu_count;
+    if (clk) *clk = rt->clock_khz;
+    return T0_OK;
+}
+
+int t0_code_object(const void** data, size_t* size) {
+    if (!data || !size) return fail(T0_ERR_INVALID, "null argument");
+    *data = t0_hsaco_start;
+    *size = (size_t)(t0_hsaco_end - t0_hsaco_start);
+    return T0_OK;
+}
+
+int t0_generate(const t0_gemm_config* cfg, char* symbol, size_t len) {
+    if (!cfg) return fail(T0_ERR_INVALID, "null config");
+    std::string why;
+    if (!config_valid(*cfg, &why)) return fail(T0_ERR_INFEASIBLE, "%s: %s", config_name(*cfg).c_str(), why.c_str());
+    const std::string s = instance_for(*cfg)->symbol(cfg->transpose == T0_NN);
+    if (symbol && len) snprintf(symbol, len, "%s", s.c_str());
+    return T0_OK;
+}
+
+int t0_kernel_load(t0_runtime* rt, const void* co, size_t size, const char* symbol, const t0_kernel_load_config* cfg,
+                   t0_kernel** out) {
+    if (!rt || !co || !symbol || !out || !cfg) return fail(T0_ERR_INVALID, "null argument");
+    (void)size;
+    int r = set_dev(rt);
+    if (r) return r;
+    auto* k = new t0_kernel();
+    k->kind = KK_RAW;
+    if (co == (const void*)t0_hsaco_start) {
+        r = get_fn(rt, symbol, &k->fn);
+        if (r) { delete k; return r; }
+    } else {
+        hipError_t e = hipModuleLoadData(&k->own_module, co);
+        if (e != hipSuccess) { delete k; return fail(T0_ERR_HIP, "hipModuleLoadData: %s", hipGetErrorString(e)); }
+        e = hipModuleGetFunction(&k->fn, k->own_module, symbol);
+        if (e != hipSuccess) {
+            hipModuleUnload(k->own_module);
+            delete k;
+            return fail(T0_ERR_NOT_FOUND, "kernel %s not in code object", symbol);
+        }
+    }
+    memcpy(k->wg, cfg->workgroup_size, sizeof k->wg);
+    for (auto& w : k->wg) if (!w) w = 1;
+    k->lds = cfg->lds_size;
+    k->kernarg_size = cfg->kernarg_size;
+    k->name = symbol;
+    std::lock_guard<std::mutex> g(rt->mu);
+    std::string key = "raw:" + k->name + ":" + std::to_string((uintptr_t)co);
+    auto it = rt->cache.find(key);
+    if (it != rt->cache.end()) {   // cached kernels live until runtime destroy
+        if (k->own_module) hipModuleUnload(k->own_module);
+        delete k;
+        *out = it->second;
+        return T0_OK;
+    }
+    rt->cache[key] = k;
+    *out = k;
+    return T0_OK;
+}
+
+int t0_ensure_kernel(t0_runtime* rt, const t0_gemm_config* cfg, t0_kernel** out) {
+    if (!rt || !cfg || !out) return fail(T0_ERR_INVALID, "null argument");
+    const std::string name = config_name(*cfg);
+    {
+        std::lock_guard<std::mutex> g(rt->mu);
+        auto it = rt->cache.find(name);
+        if (it != rt->cache.end()) { *out = it->second; return T0_OK; }
+    }
+    std::string why;
+    if (!config_valid(*cfg, &why)) return fail(T0_ERR_INFEASIBLE, "%s: %s", name.c_str(), why.c_str());
+    int r = set_dev(rt);
+    if (r) return r;
+    auto* k = new t0_kernel();
+    k->kind = KK_GEMM_GEN;
+    k->inst = instance_for(*cfg);
+    k->cfg = *cfg;
+    k->name = name;
+    k->wg[0] = cfg->wg_size;
+    k->lds = k->inst->lds_bytes();
+    k->kernarg_size = cfg->epilogue == T0_EPI_STORE_F32 ? 40 : 48;
+    r = get_fn(rt, k->inst->symbol(cfg->transpose == T0_NN), &k->fn);
+    if (r) { delete k; return r; }
+    std::lock_guard<std::mutex> g(rt->mu);
+    rt->cache[name] = k;
+    *out = k;
+    return T0_OK;
+}
+
+int t0_ensure_tile_kernel(t0_runtime* rt, const t0_tile_gemm* spec, t0_kernel** out) {
+    if (!rt || !spec || !out) return fail(T0_ERR_INVALID, "null argument");
+    const std::string name = tile_name(*spec);
+    {
+        std::lock_guard<std::mutex> g(rt->mu);
+        auto it = rt->cache.find(name);
+        if (it != rt->cache.end()) { *out = it->second; return T0_OK; }
+    }
+    const GemmInstance* inst = tile_instance(*spec);
+    if (!inst) return fail(T0_ERR_INFEASIBLE, "%s: no gfx950 kernel for this tile", name.c_str());
+    if (spec->split_k > 1 && (spec->out_dtype == T0_OUT_BF16 || spec->n_epilogue))
+        return fail(T0_ERR_INFEASIBLE, "%s: split-K planes must be f32 without epilogue", name.c_str());
+    int r = set_dev(rt);
+    if (r) return r;
+    auto* k = new t0_kernel();
+    k->kind = KK_TILE;
+    k->inst = inst;
+    k->tile = *spec;
+    k->layout = tile_arg_layout(*spec);
+    k->name = name;
+    k->wg[0] = inst->threads();
+    k->lds = inst->lds_bytes();
+    k->kernarg_size = k->layout.size;
+    r = get_fn(rt, inst->symbol(spec->transpose == T0_NN), &k->fn);
+    if (r) { delete k; return r; }
+    std::lock_guard<std::mutex> g(rt->mu);
+    rt->cache[name] = k;
+    *out = k;
+    return T0_OK;
+}
+
+int t0_get_kernel(t0_runtime* rt, const char* name, t0_kernel** out) {
+    if (!rt || !name || !out) return fail(T0_ERR_INVALID, "null argument");
+    std::lock_guard<std::mutex> g(rt->mu);
+    auto it = rt->cache.find(name);
+    if (it == rt->cache.end()) return fail(T0_ERR_NOT_FOUND, "kernel %s not loaded", name);
+    *out = it->second;
+    return T0_OK;
+}
+
+int t0_kernel_info(const t0_kernel* k, uint32_t wg[3], uint32_t* lds, uint32_t* ka, char* name, size_t len) {
+    if (!k) return fail(T0_ERR_INVALID, "null kernel");
+    if (wg) memcpy(wg, k->wg, sizeof k->wg);
+    if (lds) *lds = k->lds;
+    if (ka) *ka = k->kernarg_size;
+    if (name && len) snprintf(name, len, "%s", k->name.c_str());
+    return T0_OK;
+}
+
+static int dispatch_impl(t0_runtime* rt, const t0_kernel* k, const uint32_t grid[3], const void* ka, size_t len) {
+    if (!rt || !k || !grid) return fail(T0_ERR_INVALID, "null argument");
+    if (rt->poisoned.load())
+        return fail(T0_ERR_POISONED, "queue poisoned after GPU failure -- refusing dispatch");   // gpu_context.rs:311-313
+    if (k->kernarg_size && len != k->kernarg_size)                                               // gpu_context.rs:319-322
+        return fail(T0_ERR_KERNARG, "kernarg mismatch: builder produced %zuB, kernel %s declares %uB", len,
+                    k->name.c_str(), k->kernarg_size);
+    if (len && !ka) return fail(T0_ERR_INVALID, "null kernargs");
+    int r = set_dev(rt);
+    if (r) return r;
+    const uint8_t* b = (const uint8_t*)ka;
+    for (int d = 0; d < 3; d++)
+        if (grid[d] % k->wg[d]) return fail(T0_ERR_INVALID, "grid[%d]=%u is not a multiple of the workgroup size %u", d, grid[d], k->wg[d]);
+    const uint32_t bx = grid[0] / k->wg[0], by = grid[1] / k->wg[1], bz = grid[2] / k->wg[2];
+
+    if (k->kind == KK_RAW) {
+        if (rt->poisoned.load()) return fail(T0_ERR_POISONED, "poisoned");
+        size_t sz = len;
+        void* cfgv[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, const_cast<void*>(ka), HIP_LAUNCH_PARAM_BUFFER_SIZE, &sz,
+                        HIP_LAUNCH_PARAM_END};
+        HIPCHK(hipModuleLaunchKernel(k->fn, bx, by, bz, k->wg[0], k->wg[1], k->wg[2], 0, rt->stream, nullptr, cfgv));
+        return T0_OK;
+    }
+    t0_gemm_params p;
+    memset(&p, 0, sizeof p);
+    p.A = (const void*)rd64(b);
+    p.B = (const void*)rd64(b + 8);
+    p.C = (void*)rd64(b + 16);
+    p.K = rd32(b + 24);
+    p.N = rd32(b + 28);
+    p.y_split_stride = rd32(b + 36);
+    bool nn;
+    if (k->kind == KK_GEMM_GEN) {
+        const t0_gemm_config& c = k->cfg;
+        const uint32_t sk = split_of(c);
+        // gemm_gen kernels carry no M: the grid gives the M tiles
+        // (src/t0/gemm_gen.rs:308-329; M % tile_m == 0 there).
+        const uint32_t tiles_m = c.swap_grid ? by / sk : bx;
+        p.M = tiles_m * c.tile_m;
+        p.split_k = sk;
+        p.flags = c.out_dtype == T0_OUT_BF16 ? T0_GEMM_OUT_BF16 : 0;
+        p.epi_ops = epi_ops_from_gemm_gen(c.epilogue);
+        if (len >= 48) p.bias = (const float*)rd64(b + 40);
+        nn = c.transpose == T0_NN;
+    } else {
+        const t0_tile_gemm& s = k->tile;
+        const uint32_t shift = rd32(b + 32);
+        p.M = rd32(b + 40);
+        p.split_k = 1u << std::min(shift, 4u);
+        p.flags = s.out_dtype == T0_OUT_BF16 ? T0_GEMM_OUT_BF16 : 0;
+        p.epi_ops = tile_epi_ops(s);
+        if (k->layout.has_bias) p.bias = (const float*)rd64(b + k->layout.bias_off);
+        if (k->layout.has_scale) p.epi_scale = rdf(b + k->layout.scale_off);
+        if (k->layout.has_clamp) { p.clamp_lo = rdf(b + k->layout.clamp_off); p.clamp_hi = rdf(b + k->layout.clamp_off + 4); }
+        nn = s.transpose == T0_NN;
+    }
+    p.lda = p.K;
+    p.ldb = nn ? p.N : p.K;
+    p.ldc = p.N;
+    if (p.split_k > 1 && p.K % p.split_k) return fail(T0_ERR_INVALID, "K=%u not divisible by split_k=%u", p.K, p.split_k);
+    return run_gemm_params(rt, k->inst, nn, p);
+}
+
+int t0_dispatch(t0_runtime* rt, const t0_kernel* k, const uint32_t grid[3], const void* ka, size_t len) {
+    int r = dispatch_impl(rt, k, grid, ka, len);
+    if (r) return r;
+    hipError_t e = hipStreamSynchronize(rt->stream);
+    if (e != hipSuccess) {   // src/ignis/gpu_context.rs:352-355
+        t0_runtime_mark_poisoned(rt);
+        return fail(T0_ERR_HIP, "wait failed: %s", hipGetErrorString(e));
+    }
+    return T0_OK;
+}
+
+int t0_dispatch_async(t0_runtime* rt, const t0_kernel* k, const uint32_t grid[3], const void* ka, size_t len) {
+    int r = dispatch_impl(rt, k, grid, ka, len);
+    if (r) return r;
+    return (int)(rt->slot++ % 256);
+}
+
+int t0_wait_idle(t0_runtime* rt) {
+    if (!rt) return fail(T0_ERR_INVALID, "null runtime");
+    hipError_t e = hipStreamSynchronize(rt->stream);
+    if (e != hipSuccess) { t0_runtime_mark_poisoned(rt); return fail(T0_ERR_HIP, "%s", hipGetErrorString(e)); }
+    return T0_OK;
+}
+int t0_synchronize(t0_runtime* rt) { return t0_wait_idle(rt); }
+
+// ---------------------------------------------------------------- memory --
+int t0_alloc(t0_runtime* rt, size_t bytes, t0_buffer** out) {
+    if (!rt || !out) return fail(T0_ERR_INVALID, "null argument");
+    int r = set_dev(rt);
+    if (r) return r;
+    const size_t rounded = std::max<size_t>(4096, (bytes + 4095) & ~(size_t)4095);
+    {
+        std::lock_guard<std::mutex> g(rt->mu);
+        auto it = rt->pool.find(rounded);
+        if (it != rt->pool.end() && !it->second.empty()) {
+            t0_buffer* b = it->second.back();
+            it->second.pop_back();
+            b->size = bytes;
+            HIPCHK(hipMemsetAsync(b->ptr, 0, b->alloc_size, rt->stream));   // zeroed on reuse
+            HIPCHK(hipStreamSynchronize(rt->stream));
+            *out = b;
+            return T0_OK;
+        }
+    }
+    auto* b = new t0_buffer();
+    b->rt = rt;
+    b->size = bytes;
+    b->alloc_size = rounded;
+    hipError_t e = hipMalloc(&b->ptr, rounded);
+    if (e != hipSuccess) { delete b; return fail(T0_ERR_HIP, "hipMalloc(%zu): %s", rounded, hipGetErrorString(e)); }
+    *out = b;
+    return T0_OK;
+}
+
+int t0_recycle(t0_runtime* rt, t0_buffer* b) {
+    if (!rt || !b) return fail(T0_ERR_INVALID, "null argument");
+    std::lock_guard<std::mutex> g(rt->mu);
+    rt->pool[b->alloc_size].push_back(b);
+    return T0_OK;
+}
+
+int t0_buffer_free(t0_buffer* b) {
+    if (!b) return T0_OK;
+    hipFree(b->ptr);
+    delete b;
+    return T0_OK;
+}
+
+uint64_t t0_buffer_addr(const t0_buffer* b) { return b ? (uint64_t)b->ptr : 0; }
+size_t t0_buffer_size(const t0_buffer* b) { return b ? b->size : 0; }
+
+int t0_buffer_write(t0_buffer* b, size_t off, const void* src, size_t len) {
+    if (!b || (!src && len) || off + len > b->alloc_size) return fail(T0_ERR_INVALID, "write out of range");
+    HIPCHK(hipMemcpy((char*)b->ptr + off, src, len, hipMemcpyHostToDevice));
+    return T0_OK;
+}
+
+int t0_buffer_read(const t0_buffer* b, size_t off, void* dst, size_t len) {
+    if (!b || (!dst && len) || off + len > b->alloc_size) return fail(T0_ERR_INVALID, "read out of range");
+    HIPCHK(hipStreamSynchronize(b->rt->stream));
+    HIPCHK(hipMemcpy(dst, (const char*)b->ptr + off, len, hipMemcpyDeviceToHost));
+    return T0_OK;
+}
+
+int t0_buffer_zero(t0_buffer* b) {
+    if (!b) return fail(T0_ERR_INVALID, "null buffer");
+    HIPCHK(hipMemsetAsync(b->ptr, 0, b->alloc_size, b->rt->stream));
+    HIPCHK(hipStreamSynchronize(b->rt->stream));
+    return T0_OK;
+}
+
+int t0_read_f32(const t0_buffer* b, float* dst, size_t count) { return t0_buffer_read(b, 0, dst, count * 4); }
+
+int t0_memcpy_h2d(t0_runtime* rt, uint64_t dst, const void* src, size_t len) {
+    if (!rt) return fail(T0_ERR_INVALID, "null runtime");
+    HIPCHK(hipStreamSynchronize(rt->stream));
+    HIPCHK(hipMemcpy((void*)dst, src, len, hipMemcpyHostToDevice));
+    return T0_OK;
+}
+
+int t0_memcpy_d2h(t0_runtime* rt, void* dst, uint64_t src, size_t len) {
+    if (!rt) return fail(T0_ERR_INVALID, "null runtime");
+    HIPCHK(hipStreamSynchronize(rt->stream));
+    HIPCHK(hipMemcpy(dst, (const void*)src, len, hipMemcpyDeviceToHost));
+    return T0_OK;
+}
+
+int t0_memset_d(t0_runtime* rt, uint64_t dst, int value, size_t len) {
+    if (!rt) return fail(T0_ERR_INVALID, "null runtime");
+    HIPCHK(hipMemsetAsync((void*)dst, value, len, rt->stream));
+    return T0_OK;
+}
+
+int t0_event_create(t0_event** out) {
+    if (!out) return fail(T0_ERR_INVALID, "null output");
+    auto* e = new t0_event();
+    hipError_t r = hipEventCreate(&e->ev);
+    if (r != hipSuccess) { delete e; return fail(T0_ERR_HIP, "hipEventCreate: %s", hipGetErrorString(r)); }
+    *out = e;
+    return T0_OK;
+}
+int t0_event_destroy(t0_event* e) {
+    if (e) { hipEventDestroy(e->ev); delete e; }
+    return T0_OK;
+}
+int t0_event_record(t0_runtime* rt, t0_event* e) {
+    if (!rt || !e) return fail(T0_ERR_INVALID, "null argument");
+    HIPCHK(hipEventRecord(e->ev, rt->stream));
+    return T0_OK;
+}
+int t0_event_synchronize(t0_event* e) {
+    if (!e) return fail(T0_ERR_INVALID, "null event");
+    HIPCHK(hipEventSynchronize(e->ev));
+    return T0_OK;
+}
+int t0_event_elapsed_ms(const t0_event* a, const t0_event* b, float* ms) {
+    if (!a || !b || !ms) return fail(T0_ERR_INVALID, "null argument");
+    HIPCHK(hipEventElapsedTime(ms, a->ev, b->ev));
+    return T0_OK;
+}
+
+// ------------------------------------------------------------ high level --
+static int desc_to_params(const t0_gemm_desc* d, const t0_gemm_config& c, t0_gemm_params& p) {
+    memset(&p, 0, sizeof p);
+    p.A = (const void*)d->a;
+    p.B = (const void*)d->b;
+    p.C = (void*)d->c;
+    p.bias = (const float*)d->bias;
+    p.M = d->m; p.N = d->n; p.K = d->k;
+    const bool nn = d->transpose == T0_NN;
+    p.lda = d->lda ? d->lda : d->k;
+    p.ldb = d->ldb ? d->ldb : (nn ? d->n : d->k);
+    p.ldc = d->ldc ? d->ldc : d->n;
+    p.split_k = split_of(c);
+    p.flags = d->out_dtype == T0_OUT_BF16 ? T0_GEMM_OUT_BF16 : 0;
+    uint32_t ops = 0;
+    for (uint32_t i = 0; i < d->n_epilogue && i < 8; i++) {
+        if (d->epilogue[i] == 0 || d->epilogue[i] > 8) return fail(T0_ERR_INVALID, "bad epilogue op %u", d->epilogue[i]);
+        ops |= (uint32_t)d->epilogue[i] << (4 * i);
+    }
+    p.epi_ops = ops;
+    p.epi_scale = d->scale;
+    p.clamp_lo = d->clamp_min;
+    p.clamp_hi = d->clamp_max;
+    // split-K in t0_gemm always reduces in-kernel (one output, epilogue once)
+    if (p.split_k > 1) p.flags |= T0_GEMM_FIXUP;
+    if (p.lda < p.K || p.ldc < p.N || p.ldb < (nn ? p.N : p.K)) return fail(T0_ERR_INVALID, "leading dimension too small");
+    return T0_OK;
+}
+
+int t0_gemm_select(t0_runtime* rt, const t0_gemm_desc* d, t0_gemm_config* out) {
+    if (!rt || !d || !out) return fail(T0_ERR_INVALID, "null argument");
+    auto& T = tuner();
+    const std::string key = tune_key(rt, d->m, d->n, d->k, d->transpose, d->out_dtype);
+    {
+        std::lock_guard<std::mutex> g(T.mu);
+        auto it = T.mem.find(key);
+        if (it != T.mem.end()) { *out = it->second.first; return T0_OK; }
+    }
+    double tf;
+    if (load_cache(key, out, &tf)) {
+        std::lock_guard<std::mutex> g(T.mu);
+        T.mem[key] = {*out, tf};
+        return T0_OK;
+    }
+    auto c = rank_candidates(d->m, d->n, d->k, d->transpose, d->out_dtype, true);
+    if (c.empty()) return fail(T0_ERR_INFEASIBLE, "no candidate for %ux%ux%u", d->m, d->n, d->k);
+    *out = c.front().cfg;
+    return T0_OK;
+}
+
+int t0_gemm(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm_desc* d) {
+    if (!rt || !d) return fail(T0_ERR_INVALID, "null argument");
+    if (!d->m || !d->n || !d->k) return fail(T0_ERR_INVALID, "empty GEMM %ux%ux%u", d->m, d->n, d->k);
+    if (d->transpose > T0_NN || d->out_dtype > T0_OUT_BF16) return fail(T0_ERR_INVALID, "bad layout / out_dtype");
+    t0_gemm_config c;
+    if (cfg) c = *cfg;
+    else {
+        int r = t0_gemm_select(rt, d, &c);
+        if (r) return r;
+    }
+    const GemmInstance* g = instance_for(c);
+    if (!g) return fail(T0_ERR_INFEASIBLE, "%s: no gfx950 kernel", config_name(c).c_str());
+    const uint32_t sk = split_of(c);
+    if (sk > 16 || (sk & (sk - 1))) return fail(T0_ERR_INVALID, "split_k must be a power of two <= 16");
+    t0_gemm_params p;
+    int r = desc_to_params(d, c, p);
+    if (r) return r;
+    r = set_dev(rt);
+    if (r) return r;
+    if (p.split_k > 1 && !fast_ok(p, d->transpose == T0_NN, false)) p.split_k = 1, p.flags &= ~T0_GEMM_FIXUP;
+    return run_gemm_params(rt, g, d->transpose == T0_NN, p);
+}
+
+// ------------------------------------------------------------------ tuner --
+int t0_tuner_set_cache_dir(const char* dir) {
+    std::lock_guard<std::mutex> g(tuner().mu);
+    tuner().dir = dir ? dir : "";
+    tuner().mem.clear();
+    return T0_OK;
+}
+
+int t0_tuner_set_params(uint32_t max_candidates, uint32_t n_iters) {
+    std::lock_guard<std::mutex> g(tuner().mu);
+    if (max_candidates) tuner().max_candidates = max_candidates;
+    if (n_iters) tuner().n_iters = n_iters;
+    return T0_OK;
+}
+
+// 256^3 smoke test of one candidate (src/t0/auto_gemm.rs:223-272): small
+// integer data (exact in bf16 and in the f32 sums) checked at sampled points
+// against the exact integer product.
+static int smoke_256(t0_runtime* rt, const t0_gemm_config& c, uint32_t tr, uint32_t od, bool* ok) {
+    const uint32_t S = 256;
+    std::vector<uint16_t> a(S * S), b(S * S);
+    auto bf = [](int v) { float f = (float)v; uint32_t u; memcpy(&u, &f, 4); return (uint16_t)(u >> 16); };
+    for (uint32_t i = 0; i < S * S; i++) { a[i] = bf((int)(i % 7) - 3); b[i] = bf((int)(i % 5) - 2); }
+    void *da, *db, *dc;
+    HIPCHK(hipMalloc(&da, S * S * 2));
+    HIPCHK(hipMalloc(&db, S * S * 2));
+    HIPCHK(hipMalloc(&dc, S * S * 4));
+    HIPCHK(hipMemcpy(da, a.data(), S * S * 2, hipMemcpyHostToDevice));
+    HIPCHK(hipMemcpy(db, b.data(), S * S * 2, hipMemcpyHostToDevice));
+    HIPCHK(hipMemset(dc, 0, S * S * 4));
+    t0_gemm_desc d;
+    memset(&d, 0, sizeof d);
+    d.a = (uint64_t)da; d.b = (uint64_t)db; d.c = (uint64_t)dc;
+    d.m = d.n = d.k = S;
+    d.transpose = tr;
+    d.out_dtype = od;
+    int r = t0_gemm(rt, &c, &d);
+    std::vector<float> cf(S * S);
+    std::vector<uint16_t> ch(S * S);
+    if (!r) {
+        hipStreamSynchronize(rt->stream);
+        if (od == T0_OUT_BF16) hipMemcpy(ch.data(), dc, S * S * 2, hipMemcpyDeviceToHost);
+        else hipMemcpy(cf.data(), dc, S * S * 4, hipMemcpyDeviceToHost);
+    }
+    hipFree(da); hipFree(db); hipFree(dc);
+    if (r) { *ok = false; return T0_OK; }
+    *ok = true;
+    auto av = [&](uint32_t i, uint32_t kk) { return (int)((i * S + kk) % 7) - 3; };
+    auto bv = [&](uint32_t j, uint32_t kk) {   // B element for output column j
+        const uint32_t idx = tr == T0_NN ? kk * S + j : j * S + kk;
+        return (int)(idx % 5) - 2;
+    };
+    for (uint32_t t = 0; t < 72; t++) {
+        const uint32_t idx = t < 16 ? t * S + t : ((t - 16) * 331 + 97) % (S * S);
+        const uint32_t i = idx / S, j = idx % S;
+        long exact = 0;
+        for (uint32_t kk = 0; kk < S; kk++) exact += (long)av(i, kk) * bv(j, kk);
+        float got;
+        if (od == T0_OUT_BF16) { uint32_t u = (uint32_t)ch[idx] << 16; memcpy(&got, &u, 4); }
+        else got = cf[idx];
+        if (std::fabs(got - (float)exact) > (od == T0_OUT_BF16 ? std::fabs((float)exact) / 128.0f + 0.5f : 0.0f)) {
+            *ok = false;
+            break;
+        }
+    }
+    return T0_OK;
+}
+
+int t0_tune(t0_runtime* rt, uint32_t m, uint32_t n, uint32_t k, uint32_t tr, uint32_t od, t0_gemm_config* cfg_out,
+            double* tflops_out) {
+    if (!rt || !m || !n || !k) return fail(T0_ERR_INVALID, "bad arguments");
+    auto& T = tuner();
+    const std::string key = tune_key(rt, m, n, k, tr, od);
+    {
+        std::lock_guard<std::mutex> g(T.mu);
+        auto it = T.mem.find(key);
+        if (it != T.mem.end()) {
+            if (cfg_out) *cfg_out = it->second.first;
+            if (tflops_out) *tflops_out = it->second.second;
+            return T0_OK;
+        }
+    }
+    t0_gemm_config cached;
+    double tf = 0;
+    if (load_cache(key, &cached, &tf)) {
+        std::lock_guard<std::mutex> g(T.mu);
+        T.mem[key] = {cached, tf};
+        if (cfg_out) *cfg_out = cached;
+        if (tflops_out) *tflops_out = tf;
+        return T0_OK;
+    }
+    int r = set_dev(rt);
+    if (r) return r;
+    auto ranked = rank_candidates(m, n, k, tr, od, true);
+    // candidate list: best-ranked, at most two split factors per tile
+    std::vector<t0_gemm_config> cands;
+    std::map<std::string, int> per_tile;
+    for (const auto& c : ranked) {
+        if (cands.size() >= T.max_candidates) break;
+        const std::string tile = std::to_string(c.cfg.tile_m) + "x" + std::to_string(c.cfg.tile_n) + "x" + std::to_string(c.cfg.tile_k);
+        if (per_tile[tile]++ >= 2) continue;
+        cands.push_back(c.cfg);
+    }
+    void *da, *db, *dc;
+    const size_t ob = od == T0_OUT_BF16 ? 2 : 4;
+    HIPCHK(hipMalloc(&da, (size_t)m * k * 2));
+    HIPCHK(hipMalloc(&db, (size_t)n * k * 2));
+    HIPCHK(hipMalloc(&dc, (size_t)m * n * ob));
+    HIPCHK(hipMemset(da, 0x3c, (size_t)m * k * 2));
+    HIPCHK(hipMemset(db, 0x3c, (size_t)n * k * 2));
+    t0_gemm_desc d;
+    memset(&d, 0, sizeof d);
+    d.a = (uint64_t)da; d.b = (uint64_t)db; d.c = (uint64_t)dc;
+    d.m = m; d.n = n; d.k = k;
+    d.transpose = tr;
+    d.out_dtype = od;
+    hipEvent_t e0, e1;
+    hipEventCreate(&e0);
+    hipEventCreate(&e1);
+    double best_us = 1e30;
+    t0_gemm_config best = cands.empty() ? t0_gemm_config{} : cands[0];
+    for (const auto& c : cands) {
+        bool ok = false;
+        if (smoke_256(rt, c, tr, od, &ok) || !ok) {
+            fprintf(stderr, "[autotune] %s -> SKIP (256^3 check failed)\n", config_name(c).c_str());
+            continue;
+        }
+        if (t0_gemm(rt, &c, &d)) continue;   // warmup
+        std::vector<float> times;
+        for (uint32_t it = 0; it < T.n_iters; it++) {
+            hipEventRecord(e0, rt->stream);
+            if (t0_gemm(rt, &c, &d)) break;
+            hipEventRecord(e1, rt->stream);
+            hipEventSynchronize(e1);
+            float ms = 0;
+            hipEventElapsedTime(&ms, e0, e1);
+            times.push_back(ms);
+        }
+        if (times.empty()) continue;
+        std::sort(times.begin(), times.end());
+        const double us = times[times.size() / 2] * 1e3;
+        if (us < best_us) { best_us = us; best = c; }
+    }
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    hipFree(da); hipFree(db); hipFree(dc);
+    if (best_us >= 1e30) {   // src/t0/auto_gemm.rs:125-167: fall back to the static choice
+        int rr = t0_auto_select_legacy(m, k, n, &best);
+        if (rr) return rr;
+        tf = 0;
+    } else {
+        tf = 2.0 * m * n * k / (best_us * 1e-6) / 1e12;
+        save_cache(key, best, tf);
+    }
+    {
+        std::lock_guard<std::mutex> g(T.mu);
+        T.mem[key] = {best, tf};
+    }
+    if (cfg_out) *cfg_out = best;
+    if (tflops_out) *tflops_out = tf;
+    return T0_OK;
+}
+
+int t0_auto_gemm(t0_runtime* rt, uint64_t a, uint64_t b, uint64_t c, uint32_t m, uint32_t n, uint32_t k, double* tflops) {
+    t0_gemm_config cfg;
+    int r = t0_tune(rt, m, n, k, T0_NT, T0_OUT_F32, &cfg, tflops);
+    if (r) return r;
+    t0_gemm_desc d;
+    memset(&d, 0, sizeof d);
+    d.a = a; d.b = b; d.c = c;
+    d.m = m; d.n = n; d.k = k;
+    r = t0_gemm(rt, &cfg, &d);
+    if (r) return r;
+    return t0_wait_idle(rt);
+}
+
+// ------------------------------------------------------------------- INT4 --
+int t0_gptq_from_bytes(const void* raw, size_t len, t0_gptq_view* o) {
+    // src/t0/quant_kernels.rs:251-287
+    if (!raw || !o) return fail(T0_ERR_INVALID, "null argument");
+    if (len < 12) return fail(T0_ERR_INVALID, "GPTQ data too short (need at least 12 bytes header)");
+    const uint8_t* b = (const uint8_t*)raw;
+    o->rows = rd32(b);
+    o->cols = rd32(b + 4);
+    o->group_size = rd32(b + 8);
+    if (!o->group_size) return fail(T0_ERR_INVALID, "group_size 0");
+    o->n_groups = o->cols / o->group_size;
+    const size_t n_params = (size_t)o->n_groups * o->rows;
+    const size_t packed = (size_t)o->rows * o->cols / 2;
+    const size_t need = 12 + packed + n_params * 8;
+    if (len < need) return fail(T0_ERR_INVALID, "GPTQ data truncated: need %zu bytes, got %zu", need, len);
+    o->packed = b + 12;
+    o->scales = (const float*)(b + 12 + packed);
+    o->zero_points = (const int32_t*)(b + 12 + packed + n_params * 4);
+    return T0_OK;
+}
+
+size_t t0_gptq_gpu_buffer_size(const t0_gptq_view* w) {
+    // src/t0/quant_kernels.rs:289-296
+    if (!w) return 0;
+    return (size_t)w->rows * w->cols / 2 + (size_t)w->n_groups * w->rows * 8;
+}
+
+int t0_gptq_to_w4a16(const t0_gptq_view* w, uint32_t* qweight, void* scales, int scales_f32, uint32_t* zeros) {
+    if (!w || !qweight || !scales) return fail(T0_ERR_INVALID, "null argument");
+    if (w->cols % 8 || (zeros && w->rows % 8)) return fail(T0_ERR_INVALID, "cols %% 8 (and rows %% 8 for zeros) required");
+    memcpy(qweight, w->packed, (size_t)w->rows * w->cols / 2);
+    const uint32_t G = w->n_groups, N = w->rows;
+    if (zeros) memset(zeros, 0, (size_t)G * (N / 8) * 4);
+    for (uint32_t n = 0; n < N; n++)
+        for (uint32_t g = 0; g < G; g++) {
+            const float s = w->scales[(size_t)n * G + g];
+            if (scales_f32) ((float*)scales)[(size_t)g * N + n] = s;
+            else {
+                uint32_t u;
+                memcpy(&u, &s, 4);
+                uint16_t h;
+                if ((u & 0x7FFFFFFFu) > 0x7F800000u) h = (uint16_t)((u >> 16) | 0x40);
+                else h = (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1)) >> 16);
+                ((uint16_t*)scales)[(size_t)g * N + n] = h;
+            }
+            if (zeros) {
+                const int32_t z = w->zero_points[(size_t)n * G + g];
+                if (z < 0 || z > 15) return fail(T0_ERR_INVALID, "zero point %d at row %u group %u not in 0..15", z, n, g);
+                zeros[(size_t)g * (N / 8) + n / 8] |= (uint32_t)z << (4 * (n % 8));
+            }
+        }
+    return T0_OK;
+}
+
+int t0_dequant_int4(t0_runtime* rt, uint64_t packed, uint64_t scales, uint64_t zp, uint64_t output, uint32_t rows,
+                    uint32_t cols, uint32_t gs_log2, int bf16_out) {
+    if (!rt || !packed || !scales || !zp || !output) return fail(T0_ERR_INVALID, "null argument");
+    if (gs_log2 > 16 || ((uint64_t)rows * cols) % 2) return fail(T0_ERR_INVALID, "bad shape");
+    int r = set_dev(rt);
+    if (r) return r;
+    hipFunction_t f;
+    r = get_fn(rt, bf16_out ? "dequant_int4_bf16" : "dequant_int4_f32", &f);
+    if (r) return r;
+    t0_dequant_params p;
+    memset(&p, 0, sizeof p);
+    p.packed = (const uint8_t*)packed;
+    p.scales = (const float*)scales;
+    p.zero_points = (const int32_t*)zp;
+    p.output = (void*)output;
+    p.rows = rows;
+    p.cols = cols;
+    p.group_size_log2 = gs_log2;
+    const uint64_t total = (uint64_t)rows * cols;
+    return launch(rt, f, (uint32_t)((total + 255) / 256), 1, 1, 256, p);
+}
+
+struct W4Plan {
+    std::string sym;
+    uint32_t gx = 1, gy = 1, threads = 256, split = 1;
+    int kind = 0;   // 0 generic, 1 decode, 2 prefill
+    uint32_t bm = 0, bn = 0;
+};
+
+static int w4_plan(t0_runtime* rt, const t0_w4a16_desc* d, W4Plan& pl) {
+    (void)rt;
+    const uint32_t M = d->m, N = d->n, K = d->k, gs = d->group_size;
+    if (!M || !N || !K || !gs) return fail(T0_ERR_INVALID, "empty W4A16 problem");
+    if (K % 8 || gs % 8 || K % gs) return fail(T0_ERR_INVALID, "K %% 8, gs %% 8 and K %% gs must be 0");
+    if (d->zeros && N % 8) return fail(T0_ERR_INVALID, "packed zero points need N %% 8 == 0");
+    const uint32_t lda = d->lda ? d->lda : K, ldc = d->ldc ? d->ldc : N;
+    const bool align_ok = aligned16(d->a) && aligned16(d->qweight) && lda % 8 == 0 && aligned16(d->c) && ldc % 4 == 0 &&
+                          (d->scales % 8) == 0;
+    const bool fast = gs == 128 && K % 128 == 0 && align_ok;
+    pl = W4Plan();
+    if (fast && M <= 64 && N % 64 == 0) {
+        const uint32_t mb = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+        const uint32_t waves = (mb == 1 && N % 128 == 0) ? 8 : 4;
+        const uint32_t ncw = 16 * waves;
+        uint32_t sk = d->split_k;
+        if (!sk) {
+            // enough workgroups to cover the CUs a few times; slice <= 1024
+            sk = 1;
+            while (sk < 16 && ((uint64_t)(N / ncw) * sk < 512 || K / sk > 1024) && (K / (2 * sk)) % 128 == 0 &&
+                   K / (2 * sk) >= 128)
+                sk *= 2;
+        }
+        if (K % (128 * sk) || K / sk > 1024) return fail(T0_ERR_INVALID, "split_k %u does not fit K %u", sk, K);
+        char b[64];
+        snprintf(b, sizeof b, "t0k_w4a16_decode_w%u_mb%u", waves, mb);
+        pl.sym = b;
+        pl.gx = N / ncw;
+        pl.gy = sk;
+        pl.threads = waves * 64;
+        pl.split = sk;
+        pl.kind = 1;
+        return T0_OK;
+    }
+    if (fast && M > 64 && N % 8 == 0 && !d->scales_f32) {
+        const bool big = M >= 1024;
+        pl.bm = big ? 256 : 128;
+        pl.bn = 128;
+        char b[64];
+        snprintf(b, sizeof b, "t0k_w4a16_prefill_%ux%u_w2x2_s2", pl.bm, pl.bn);
+        pl.sym = b;
+        pl.gx = ((M + pl.bm - 1) / pl.bm) * ((N + pl.bn - 1) / pl.bn);
+        pl.threads = 256;
+        pl.kind = 2;
+        return T0_OK;
+    }
+    pl.sym = "t0k_w4a16_generic";
+    pl.gx = (N + 255) / 256;
+    pl.gy = M;
+    pl.threads = 256;
+    pl.kind = 0;
+    return T0_OK;
+}
+
+int t0_w4a16_plan(t0_runtime* rt, const t0_w4a16_desc* d, char* kernel, size_t len, uint32_t* split_k) {
+    if (!d) return fail(T0_ERR_INVALID, "null desc");
+    W4Plan pl;
+    int r = w4_plan(rt, d, pl);
+    if (r) return r;
+    if (kernel && len) snprintf(kernel, len, "%s", pl.sym.c_str());
+    if (split_k) *split_k = pl.split;
+    return T0_OK;
+}
+
+int t0_w4a16_gemm(t0_runtime* rt, const t0_w4a16_desc* d) {
+    if (!rt || !d || !d->a || !d->qweight || !d->scales || !d->c) return fail(T0_ERR_INVALID, "null argument");
+    W4Plan pl;
+    int r = w4_plan(rt, d, pl);
+    if (r) return r;
+    r = set_dev(rt);
+    if (r) return r;
+    t0_w4a16_params p;
+    memset(&p, 0, sizeof p);
+    p.A = (const void*)d->a;
+    p.qweight = (const uint32_t*)d->qweight;
+    p.scales = (const void*)d->scales;
+    p.zeros = (const uint32_t*)d->zeros;
+    p.C = (void*)d->c;
+    p.M = d->m; p.N = d->n; p.K = d->k;
+    p.lda = d->lda ? d->lda : d->k;
+    p.ldc = d->ldc ? d->ldc : d->n;
+    p.group_size = d->group_size;
+    p.zero_const = d->zero_const;
+    p.flags = (d->scales_f32 ? T0_W4_SCALE_F32 : 0) | (d->out_f32 ? T0_W4_OUT_F32 : 0);
+    p.split_k = pl.split;
+    if (!d->zeros && d->zero_const > 15) return fail(T0_ERR_INVALID, "zero_const must be 0..15");
+    hipFunction_t f;
+    if (pl.kind == 1 && pl.split > 1) {
+        r = ensure_ws(rt, (size_t)pl.split * p.M * p.N * 4);
+        if (r) return r;
+        r = ensure_sem(rt, pl.gx);
+        if (r) return r;
+        p.workspace = (float*)rt->ws;
+        p.semaphores = rt->sem;
+    }
+    if (pl.kind == 2) {
+        // X[g][m] = -144 * group row sums of A (plus 1 KiB tail the DMA may touch)
+        const uint32_t G = p.K / 128;
+        r = ensure_ws(rt, (size_t)G * p.M * 4 + 2048);
+        if (r) return r;
+        p.workspace = (float*)rt->ws;
+        hipFunction_t fr;
+        r = get_fn(rt, "t0k_w4a16_rowsum", &fr);
+        if (r) return r;
+        const uint32_t waves = p.M * ((G + 7) / 8);
+        r = launch(rt, fr, (waves + 3) / 4, 1, 1, 256, p);
+        if (r) return r;
+    }
+    r = get_fn(rt, pl.sym, &f);
+    if (r) return r;
+    return launch(rt, f, pl.gx, pl.gy, 1, pl.threads, p);
+}
+
+// --------------------------------------------------------- small kernels --
+int t0_splitk_reduce(t0_runtime* rt, uint64_t src, uint64_t stride, uint32_t planes, uint64_t dst, uint32_t m,
+                     uint32_t n, int out_bf16) {
+    if (!rt || !src || !dst) return fail(T0_ERR_INVALID, "null argument");
+    int r = set_dev(rt);
+    if (r) return r;
+    hipFunction_t f;
+    r = get_fn(rt, "t0k_splitk_reduce", &f);
+    if (r) return r;
+    t0_aux_params p;
+    memset(&p, 0, sizeof p);
+    p.src = (const void*)src; p.dst = (void*)dst;
+    p.m = m; p.n = n; p.ld_src = n; p.ld_dst = n;
+    p.planes = planes; p.plane_stride = stride;
+    p.flags = out_bf16 ? T0_GEMM_OUT_BF16 : 0;
+    return launch(rt, f, (uint32_t)(((uint64_t)m * n + 255) / 256), 1, 1, 256, p);
+}
+
+int t0_f32_to_bf16(t0_runtime* rt, uint64_t src, uint64_t dst, uint64_t count) {
+    if (!rt || !src || !dst) return fail(T0_ERR_INVALID, "null argument");
+    if (count > 0xFFFFFFFFull) return fail(T0_ERR_INVALID, "count too large");
+    int r = set_dev(rt);
+    if (r) return r;
+    hipFunction_t f;
+    r = get_fn(rt, "t0k_f32_to_bf16", &f);
+    if (r) return r;
+    t0_aux_params p;
+    memset(&p, 0, sizeof p);
+    p.src = (const void*)src; p.dst = (void*)dst;
+    p.m = 1; p.n = (uint32_t)count; p.ld_src = p.n; p.ld_dst = p.n;
+    return launch(rt, f, (uint32_t)((count + 255) / 256), 1, 1, 256, p);
+}
+
+int t0_unpad_2d(t0_runtime* rt, uint64_t padded, uint64_t out, uint32_t m, uint32_t n, uint32_t n_pad) {
+    if (!rt || !padded || !out || n_pad < n) return fail(T0_ERR_INVALID, "bad arguments");
+    int r = set_dev(rt);
+    if (r) return r;
+    hipFunction_t f;
+    r = get_fn(rt, "t0_unpad_2d", &f);
+    if (r) return r;
+    t0_aux_params p;
+    memset(&p, 0, sizeof p);
+    p.src = (const void*)padded; p.dst = (void*)out;
+    p.m = m; p.n = n; p.ld_src = n_pad; p.ld_dst = n;
+    return launch(rt, f, (uint32_t)(((uint64_t)m * n + 255) / 256), 1, 1, 256, p);
+}
+
+}  // extern "C"

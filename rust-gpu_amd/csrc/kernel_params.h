@@ -1,0 +1,96 @@
+// kernel_params.h -- argument blocks shared by the host runtime and the gfx950
+// kernels.  Every kernel in the code object takes exactly one of these structs
+// by value; the host runtime decodes the reference's kernarg byte layouts
+// (40/44/48-byte GEMM layouts, 40-byte dequant layout) into them.
+#pragma once
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+// Epilogue chain opcodes (one 4-bit slot each, applied low slot first).
+// Semantics follow src/t0/tile_ir.rs:41-62 / :3406-3540 of the reference.
+enum t0_epi_op {
+    T0_EPI_NONE = 0,
+    T0_EPI_BIAS = 1,   // y += bias[col]           (f32 bias vector [N])
+    T0_EPI_SCALE = 2,  // y *= scale
+    T0_EPI_RELU = 3,   // y = max(y, 0)
+    T0_EPI_SILU = 4,   // y = y * sigmoid(y)
+    T0_EPI_GELU = 5,   // y = y * sigmoid(1.702 y)  (the reference's GELU form)
+    T0_EPI_ABS = 6,    // y = |y|
+    T0_EPI_NEG = 7,    // y = -y
+    T0_EPI_CLAMP = 8,  // y = min(max(y, lo), hi)
+};
+
+#define T0_MAX_EPI_OPS 8
+
+// flags
+#define T0_GEMM_OUT_BF16 0x1u   // store bf16 (RNE) instead of f32
+#define T0_GEMM_FIXUP 0x2u      // split-K reduced in-kernel into C (workspace + semaphores)
+
+typedef struct t0_gemm_params {
+    const void* A;        // bf16 [M, lda]  row-major, k contiguous
+    const void* B;        // NT: bf16 [N, ldb] (k contiguous); NN: bf16 [K, ldb] (n contiguous)
+    void* C;              // f32 or bf16 [M, ldc] (split-K planes at C + p*y_split_stride)
+    const float* bias;    // [N] f32 (T0_EPI_BIAS)
+    float* workspace;     // fixup planes [split_k][tiles][BM*BN] f32
+    uint32_t* semaphores; // fixup counters [tiles]
+    uint32_t M, N, K;
+    uint32_t lda, ldb, ldc;
+    uint32_t split_k;          // >= 1
+    uint32_t flags;
+    uint64_t y_split_stride;   // bytes between split-K output planes
+    uint32_t epi_ops;          // packed 4-bit opcodes, 0 terminates
+    float epi_scale, clamp_lo, clamp_hi;
+} t0_gemm_params;
+
+// W4A16: C[M,N] = A[M,K] (bf16) . W^T, W given as GPTQ-packed int4
+// [N][K/8] u32 words (k at bits 4*(k%8)), scales [N][K/gs] (bf16 or f32),
+// zero points either the constant zero_const (zeros == NULL) or packed 4-bit
+// [N][ceil(G/8)] u32 words (group g at bits 4*(g%8)).
+#define T0_W4_SCALE_F32 0x1u   // scales are f32 (else bf16)
+#define T0_W4_OUT_F32 0x2u     // store f32 (else bf16 RNE)
+
+typedef struct t0_w4a16_params {
+    const void* A;            // bf16 [M, lda]
+    const uint32_t* qweight;  // [N][K/8]
+    const void* scales;       // [N][G]
+    const uint32_t* zeros;    // [N][ceil(G/8)] or NULL
+    void* C;                  // [M, ldc]
+    float* workspace;         // decode split-K partial planes
+    uint32_t* semaphores;     // decode split-K counters
+    uint32_t M, N, K;
+    uint32_t lda, ldc;
+    uint32_t group_size;      // multiple of 32 (fast kernels: 128)
+    uint32_t zero_const;
+    uint32_t flags;
+    uint32_t split_k;         // decode: K partitions (>= 1)
+    uint32_t pad_;
+} t0_w4a16_params;
+
+// Reference dequant kernel arguments (src/t0/quant_kernels.rs:45-47):
+// [packed_weights, scales(f32), zero_points(i32), output; rows, cols]
+typedef struct t0_dequant_params {
+    const uint8_t* packed;
+    const float* scales;
+    const int32_t* zero_points;
+    void* output;
+    uint32_t rows, cols;
+    uint32_t group_size_log2;
+    uint32_t pad_;
+} t0_dequant_params;
+
+typedef struct t0_aux_params {
+    const void* src;
+    void* dst;
+    uint32_t m, n;        // logical rows / cols
+    uint32_t ld_src, ld_dst;
+    uint32_t planes;      // split-K plane count (reduce)
+    uint32_t flags;       // T0_GEMM_OUT_BF16 for reduce output
+    uint64_t plane_stride;  // bytes
+} t0_aux_params;
+
+#ifdef __cplusplus
+}
+#endif

@@ -1,0 +1,99 @@
+// aux.hip -- generic-shape GEMM fallback and the small kernels around the
+// GEMM path (split-K plane reduction, f32 -> bf16 conversion, unpad).
+#include "common.h"
+
+namespace t0 {
+
+T0_DEV float ld_bf16(const uint16_t* p) { return bf16_bits_to_f32(*p); }
+
+// Generic bf16 GEMM: any M, N, K, leading dimensions and alignment; NT or NN;
+// f32/bf16 out; epilogue chain; reference split-K planes.  64x64 tile per
+// 256-thread workgroup, each wave one 32x32 block, operands gathered straight
+// from global memory with bounds checks.  Correctness fallback only.
+template <bool NN>
+__device__ __forceinline__ void gemm_generic(const t0_gemm_params& p) {
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t M = p.M, N = p.N, K = p.K;
+    const uint32_t tiles_m = (M + 63) / 64, tiles_n = (N + 63) / 64;
+    const uint32_t tiles = tiles_m * tiles_n, sk = p.split_k;
+    const uint32_t bid = blockIdx.y * gridDim.x + blockIdx.x;
+    if (bid >= tiles * sk) return;
+    const uint32_t part = bid / tiles, tile = bid % tiles;
+    const uint32_t m0 = (tile / tiles_n) * 64 + (wave / 2) * 32;
+    const uint32_t n0 = (tile % tiles_n) * 64 + (wave % 2) * 32;
+    const uint32_t k_per = K / sk, kb = part * k_per, ke = (part + 1 == sk) ? K : kb + k_per;
+    const uint16_t* A = (const uint16_t*)p.A;
+    const uint16_t* B = (const uint16_t*)p.B;
+    const uint32_t l32 = lane & 31, hi = lane >> 5;
+    const uint32_t m = m0 + l32, n = n0 + l32;
+    f32x16_t acc = {};
+    for (uint32_t k = kb; k < ke; k += 16) {
+        bf16x8_t a, b;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const uint32_t kk = k + hi * 8 + e;
+            const bool kin = kk < ke;
+            a[e] = (__bf16)((kin && m < M) ? ld_bf16(A + (size_t)m * p.lda + kk) : 0.0f);
+            float bv = 0.0f;
+            if (kin && n < N) bv = NN ? ld_bf16(B + (size_t)kk * p.ldb + n) : ld_bf16(B + (size_t)n * p.ldb + kk);
+            b[e] = (__bf16)bv;
+        }
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, a, acc, 0, 0, 0);
+    }
+    // acc[r] = C[m0 + l32][n0 + 8*(r/4) + 4*hi + r%4]
+    if (m >= M) return;
+    uint8_t* Cb = (uint8_t*)p.C + (size_t)part * p.y_split_stride;
+    const uint32_t ops = p.epi_ops;
+    const bool has_bias = ops && epi_has_bias(ops);
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const uint32_t nn = n0 + 8 * (r / 4) + 4 * hi + (r % 4);
+        if (nn >= N) continue;
+        float v = acc[r];
+        if (ops) v = apply_epilogue(v, ops, has_bias ? p.bias[nn] : 0.0f, p.epi_scale, p.clamp_lo, p.clamp_hi);
+        if (p.flags & T0_GEMM_OUT_BF16)
+            ((uint16_t*)Cb)[(size_t)m * p.ldc + nn] = (uint16_t)(pack2_bf16_rne(v, 0.f) & 0xFFFFu);
+        else
+            ((float*)Cb)[(size_t)m * p.ldc + nn] = v;
+    }
+}
+
+// C[m][n] = sum_p planes[p][m][n] in plane order (the host split-K sum of
+// examples/hello_gemm_gen.rs:125-136, on the GPU).  f32 or bf16 (RNE) out.
+__device__ __forceinline__ void splitk_reduce(const t0_aux_params& p) {
+    const uint64_t e = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= (uint64_t)p.m * p.n) return;
+    const uint32_t r = (uint32_t)(e / p.n), c = (uint32_t)(e % p.n);
+    const uint8_t* src = (const uint8_t*)p.src;
+    float v = 0.0f;
+    for (uint32_t q = 0; q < p.planes; q++)
+        v = v + ((const float*)(src + (size_t)q * p.plane_stride))[(size_t)r * p.ld_src + c];
+    if (p.flags & T0_GEMM_OUT_BF16) ((uint16_t*)p.dst)[(size_t)r * p.ld_dst + c] = (uint16_t)(pack2_bf16_rne(v, 0.f) & 0xFFFFu);
+    else ((float*)p.dst)[(size_t)r * p.ld_dst + c] = v;
+}
+
+// f32 -> bf16 round-to-nearest-even, element-wise over [m][n] with strides.
+// (The conversion src/ignis/ops/bf16_matmul.rs:356-383 runs on the CPU.)
+__device__ __forceinline__ void f32_to_bf16(const t0_aux_params& p) {
+    const uint64_t e = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= (uint64_t)p.m * p.n) return;
+    const uint32_t r = (uint32_t)(e / p.n), c = (uint32_t)(e % p.n);
+    const float v = ((const float*)p.src)[(size_t)r * p.ld_src + c];
+    ((uint16_t*)p.dst)[(size_t)r * p.ld_dst + c] = (uint16_t)(pack2_bf16_rne(v, 0.f) & 0xFFFFu);
+}
+
+// out[m][n] = padded[m][n_pad]  (src/t0/math.rs t0_unpad_2d semantics).
+__device__ __forceinline__ void unpad_2d(const t0_aux_params& p) {
+    const uint64_t e = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= (uint64_t)p.m * p.n) return;
+    const uint32_t r = (uint32_t)(e / p.n), c = (uint32_t)(e % p.n);
+    ((float*)p.dst)[(size_t)r * p.ld_dst + c] = ((const float*)p.src)[(size_t)r * p.ld_src + c];
+}
+
+}  // namespace t0
+
+extern "C" __global__ void __launch_bounds__(256) t0k_gemm_generic_nt(const t0_gemm_params p) { t0::gemm_generic<false>(p); }
+extern "C" __global__ void __launch_bounds__(256) t0k_gemm_generic_nn(const t0_gemm_params p) { t0::gemm_generic<true>(p); }
+extern "C" __global__ void __launch_bounds__(256) t0k_splitk_reduce(const t0_aux_params p) { t0::splitk_reduce(p); }
+extern "C" __global__ void __launch_bounds__(256) t0k_f32_to_bf16(const t0_aux_params p) { t0::f32_to_bf16(p); }
+extern "C" __global__ void __launch_bounds__(256) t0_unpad_2d(const t0_aux_params p) { t0::unpad_2d(p); }

@@ -1,0 +1,107 @@
+// common.h -- gfx950 device helpers shared by the GEMM kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "../kernel_params.h"
+
+#define T0_DEV __device__ __forceinline__
+#define LDS_AS __attribute__((address_space(3)))
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+namespace t0 {
+
+// ---------------------------------------------------------------- buffers --
+// Raw buffer resource (gfx9 word3 = 0x00020000).  Out-of-range offsets
+// (>= num_records) read as zero; kernels use OOB_OFFSET to mask lanes.
+constexpr uint32_t OOB_OFFSET = 0x7FFFFFF0u;
+
+T0_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
+                                             (int)OOB_OFFSET, 0x00020000);
+}
+
+// 16 bytes per lane from global (base + voffset) straight into LDS at
+// lds_wave_base + lane*16.  lds_wave_base must be wave-uniform.
+T0_DEV void load_lds_x4(__amdgpu_buffer_rsrc_t r, LDS_AS void* lds_wave_base, uint32_t voffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds_wave_base, 16, voffset, 0, 0, 0);
+}
+
+T0_DEV u32x4_t buffer_load_x4(__amdgpu_buffer_rsrc_t r, uint32_t voffset) {
+    return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, 0, 0));
+}
+
+T0_DEV uint32_t buffer_load_x1(__amdgpu_buffer_rsrc_t r, uint32_t voffset) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, voffset, 0, 0);
+}
+
+// ------------------------------------------------------------------ bf16 --
+T0_DEV float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// f32 -> bf16 round to nearest even (quiet NaN for NaN): v_cvt_pk_bf16_f32.
+T0_DEV uint32_t pack2_bf16_rne(float lo, float hi) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    bf16x2_t v;
+    v[0] = (__bf16)lo;
+    v[1] = (__bf16)hi;
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+// --------------------------------------------------------------- epilogue --
+T0_DEV float sigmoid_f(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+T0_DEV float apply_epilogue(float v, uint32_t ops, float bias_v, float scale, float lo, float hi) {
+#pragma unroll 1
+    for (; ops; ops >>= 4) {
+        switch (ops & 0xF) {
+        case T0_EPI_BIAS: v = v + bias_v; break;
+        case T0_EPI_SCALE: v = v * scale; break;
+        case T0_EPI_RELU: v = fmaxf(v, 0.0f); break;
+        case T0_EPI_SILU: v = v * sigmoid_f(v); break;
+        case T0_EPI_GELU: v = v * sigmoid_f(1.702f * v); break;
+        case T0_EPI_ABS: v = fabsf(v); break;
+        case T0_EPI_NEG: v = -v; break;
+        case T0_EPI_CLAMP: v = fminf(fmaxf(v, lo), hi); break;
+        default: break;
+        }
+    }
+    return v;
+}
+
+T0_DEV bool epi_has_bias(uint32_t ops) {
+    for (; ops; ops >>= 4)
+        if ((ops & 0xF) == T0_EPI_BIAS) return true;
+    return false;
+}
+
+// ------------------------------------------------------------- tile order --
+// Workgroups are dispatched round-robin over the 8 XCDs (workgroup b runs on
+// XCD b % 8).  Remap so that consecutive logical ids share an XCD (and its
+// L2): XCD x owns the contiguous id range [start(x), start(x) + count(x)).
+T0_DEV uint32_t xcd_remap(uint32_t b, uint32_t total) {
+    const uint32_t NX = 8;
+    uint32_t x = b % NX, i = b / NX;
+    uint32_t q = total / NX, r = total % NX;
+    uint32_t start = x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q;
+    return start + i;
+}
+
+// Grouped (super-tile) order: GROUP_M tile rows are walked column by column
+// so a run of consecutive ids covers a GROUP_M x (run/GROUP_M) block.
+T0_DEV void grouped_tile(uint32_t id, uint32_t tiles_m, uint32_t tiles_n, uint32_t group_m,
+                         uint32_t& tm, uint32_t& tn) {
+    uint32_t per_group = group_m * tiles_n;
+    uint32_t g = id / per_group;
+    uint32_t first_m = g * group_m;
+    uint32_t gm = min(tiles_m - first_m, group_m);
+    uint32_t in = id - g * per_group;
+    tm = first_m + in % gm;
+    tn = in / gm;
+}
+
+}  // namespace t0

@@ -1,0 +1,410 @@
+// gemm_bf16.hip -- tiled bf16 GEMM for gfx950 (MI355X).
+//
+//   C[M,N] = epilogue( A[M,K] . B )    bf16 in, f32 accumulate, f32 or bf16 out
+//   NT: B = WT[N,K] (k contiguous)     -- the reference's only form
+//       (src/t0/gemm_gen.rs:51-54, src/t0/tile_ir.rs:106-107)
+//   NN: B = B[K,N]  (n contiguous)     -- new; read through ds_read_b64_tr_b16
+//
+// One workgroup owns a BM x BN output tile, WM x WN waves each own a
+// (BM/WM) x (BN/WN) sub-tile built from 32x32 blocks of
+// v_mfma_f32_32x32x16_bf16.  A and B tiles move HBM -> LDS with
+// buffer_load_dwordx4 ... lds (no VGPR staging) through STAGES LDS buffers;
+// 16-byte chunks are XOR-swizzled per row so the MFMA operand reads are
+// bank-conflict free.  Rows/columns past M/N and k past K are read as zero
+// through buffer out-of-range masking, so any M, N and K (K % 8 == 0,
+// 16-byte aligned rows) is handled without host padding -- the bounds
+// behaviour of src/t0/tile_ir.rs:1142-1185 rather than gemm_gen's
+// divisibility requirement (src/t0/cost_model.rs:499-500).
+//
+// Split-K follows the reference: partition p of split_k covers
+// K-range [p*Kp, (p+1)*Kp) with Kp = K / split_k and writes a full f32 plane
+// at C + p*y_split_stride (src/t0/gemm_gen.rs:769-793).  With T0_GEMM_FIXUP
+// the partitions are instead reduced in-kernel, in plane order, by the last
+// partition to finish (deterministic), and the epilogue runs once.
+#include "common.h"
+
+namespace t0 {
+
+// Swizzle for row-major [rows][CH chunks of 16 B] tiles read 16 lanes x 16 B
+// at a time along rows (A, and B in NT form).
+template <int CH>
+T0_DEV uint32_t swz_rows(uint32_t r) {
+    if constexpr (CH >= 8) return ((r & 7) ^ ((r >> 3) & 1)) & (CH - 1);
+    else if constexpr (CH == 4) return ((r >> 1) ^ (r >> 3)) & 3;
+    else return ((r >> 2) ^ (r >> 3)) & 1;
+}
+
+// Swizzle for the NN B tile [BK][CHB chunks]: the transposed reads take four
+// consecutive k rows x 32 B per 16-lane group.
+template <int CHB>
+T0_DEV uint32_t swz_nn(uint32_t r) {
+    return (0xEA40u >> ((r & 3) * 4)) & 0xFu & (CHB - 1);   // rows 0..3 -> 0, 4, 10, 14
+}
+
+template <int BM, int BN, int BK, int WM, int WN, bool NN, int STAGES>
+struct GemmCfg {
+    static constexpr int NW = WM * WN;
+    static constexpr int NT = NW * 64;
+    static constexpr int TM = BM / WM, TN = BN / WN;
+    static constexpr int FM = TM / 32, FN = TN / 32;
+    static constexpr int A_BYTES = BM * BK * 2;
+    static constexpr int B_BYTES = BN * BK * 2;
+    static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+    static constexpr int A_LOADS = A_BYTES / (1024 * NW);  // per wave per stage
+    static constexpr int B_LOADS = B_BYTES / (1024 * NW);
+    static constexpr int LOADS = A_LOADS + B_LOADS;
+    static constexpr int CHA = BK / 8;          // 16-B chunks per A (and NT-B) row
+    static constexpr int CHB = BN / 8;          // 16-B chunks per NN-B row
+    static constexpr int EPI_LD = TN + 4;       // staged epilogue row stride (floats)
+    static constexpr int EPI_WAVE_FLOATS = 32 * EPI_LD;
+    static constexpr int SMEM_BYTES = (STAGE_BYTES * STAGES > NW * EPI_WAVE_FLOATS * 4)
+                                          ? STAGE_BYTES * STAGES : NW * EPI_WAVE_FLOATS * 4;
+    static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be 32x32 blocks");
+    static_assert(BK % 16 == 0, "BK must be a multiple of 16");
+    static_assert(A_LOADS >= 1 && A_LOADS * 1024 * NW == A_BYTES, "A tile / load split");
+    static_assert(B_LOADS >= 1 && B_LOADS * 1024 * NW == B_BYTES, "B tile / load split");
+    static_assert(STAGES >= 2, "at least double buffering");
+    static_assert(STAGE_BYTES * STAGES <= 160 * 1024, "LDS");
+};
+
+template <int N>
+T0_DEV void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+
+// 16 bytes per lane, global (rsrc + voffset) -> LDS (m0 + lane*16).  Issued
+// as inline asm: the compiler cannot see which LDS buffer the DMA targets and
+// would otherwise wait for it (vmcnt(0)) before every LDS read; the K loop
+// tracks completion itself with explicit vmcnt waits.
+T0_DEV void dma_x4(__amdgpu_buffer_rsrc_t r, uint32_t lds_addr, uint32_t voffset) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :: "s"(lds_addr), "v"(voffset), "s"(r) : "memory");
+}
+
+template <class G>
+struct TileLoader {
+    // per-lane byte offsets relative to the stage's tile base, or OOB
+    uint32_t a_off[G::A_LOADS];
+    uint32_t b_off[G::B_LOADS];
+    uint32_t a_kchunk[G::A_LOADS];  // k offset (elements) of the lane's chunk within the stage
+    uint32_t b_krow[G::B_LOADS];    // NN: k row within the stage; NT: k chunk offset
+};
+
+// Epilogue + bounds-checked store of 4 consecutive columns n..n+3 of row m.
+T0_DEV void store_quad(const t0_gemm_params& p, uint8_t* Cb, uint32_t m, uint32_t n, f32x4_t v) {
+    if (m >= p.M || n >= p.N) return;
+    const uint32_t N = p.N;
+    const uint32_t ops = p.epi_ops;
+    if (ops) {
+        const bool has_bias = epi_has_bias(ops);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            float bv = (has_bias && n + e < N) ? p.bias[n + e] : 0.0f;
+            v[e] = apply_epilogue(v[e], ops, bv, p.epi_scale, p.clamp_lo, p.clamp_hi);
+        }
+    }
+    if (p.flags & T0_GEMM_OUT_BF16) {
+        uint16_t* dst = (uint16_t*)Cb + (size_t)m * p.ldc + n;
+        if (n + 3 < N) {
+            *(u32x2_t*)dst = u32x2_t{pack2_bf16_rne(v[0], v[1]), pack2_bf16_rne(v[2], v[3])};
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (n + e < N) dst[e] = (uint16_t)(pack2_bf16_rne(v[e], 0.0f) & 0xFFFFu);
+        }
+    } else {
+        float* dst = (float*)Cb + (size_t)m * p.ldc + n;
+        if (n + 3 < N) {
+            *(f32x4_t*)dst = v;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (n + e < N) dst[e] = v[e];
+        }
+    }
+}
+
+// Write one staged 32 x TN block (wave-private LDS, row stride EPI_LD floats)
+// to C rows [row0, row0+32), columns [col0, col0+TN), row-major, one 4-column
+// quad per lane per step.
+template <class G>
+T0_DEV void emit_rowblock(const t0_gemm_params& p, uint8_t* Cb, const float* wreg,
+                          uint32_t row0, uint32_t col0, uint32_t lane) {
+    constexpr uint32_t QPR = G::TN / 4;  // quads per row
+#pragma unroll 1
+    for (uint32_t q = lane; q < 32 * QPR; q += 64) {
+        const uint32_t r = q / QPR, c4 = q % QPR;
+        f32x4_t v = *(const LDS_AS f32x4_t*)(wreg + r * G::EPI_LD + c4 * 4);
+        store_quad(p, Cb, row0 + r, col0 + c4 * 4, v);
+    }
+}
+
+template <int BM, int BN, int BK, int WM, int WN, bool NN, int STAGES>
+__device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
+    using G = GemmCfg<BM, BN, BK, WM, WN, NN, STAGES>;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[G::SMEM_BYTES];
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63;
+    const uint32_t wave = tid >> 6;
+    const uint32_t wm = wave / WN, wn = wave % WN;
+
+    // ---- tile assignment -------------------------------------------------
+    const uint32_t M = p.M, N = p.N, K = p.K;
+    const uint32_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    const uint32_t tiles = tiles_m * tiles_n;
+    const uint32_t sk = p.split_k;
+    const uint32_t total = tiles * sk;
+    const uint32_t bid = blockIdx.y * gridDim.x + blockIdx.x;
+    if (bid >= total) return;
+    const uint32_t lid = xcd_remap(bid, total);
+    const uint32_t part = lid / tiles;
+    const uint32_t tile_id = lid % tiles;
+    uint32_t tm, tn;
+    grouped_tile(tile_id, tiles_m, tiles_n, 4, tm, tn);
+    const uint32_t m0 = tm * BM, n0 = tn * BN;
+    const uint32_t k_per = K / sk;                 // reference: k_end = K >> shift
+    const uint32_t k_begin = part * k_per;
+    const uint32_t k_end = (part + 1 == sk) ? K : k_begin + k_per;
+    const uint32_t k_len = k_end - k_begin;
+    const uint32_t nk = (k_len + BK - 1) / BK;
+
+    const uint32_t lda = p.lda, ldb = p.ldb;
+    const uint8_t* A0 = (const uint8_t*)p.A + ((size_t)m0 * lda + k_begin) * 2;
+    const uint8_t* B0 = NN ? (const uint8_t*)p.B + ((size_t)k_begin * ldb + n0) * 2
+                           : (const uint8_t*)p.B + ((size_t)n0 * ldb + k_begin) * 2;
+
+    // ---- per-lane load offsets (constant over the K loop) ------------------
+    TileLoader<G> ld;
+#pragma unroll
+    for (int j = 0; j < G::A_LOADS; j++) {
+        uint32_t pos = (wave * G::A_LOADS + j) * 1024 + lane * 16;
+        uint32_t r = pos / (BK * 2), s = (pos % (BK * 2)) / 16;
+        uint32_t c = s ^ swz_rows<G::CHA>(r);
+        bool ok = (m0 + r) < M;
+        ld.a_off[j] = ok ? r * lda * 2 + c * 16 : OOB_OFFSET;
+        ld.a_kchunk[j] = c * 8;
+    }
+#pragma unroll
+    for (int j = 0; j < G::B_LOADS; j++) {
+        uint32_t pos = (wave * G::B_LOADS + j) * 1024 + lane * 16;
+        if constexpr (NN) {
+            uint32_t r = pos / (BN * 2), s = (pos % (BN * 2)) / 16;
+            uint32_t c = s ^ swz_nn<G::CHB>(r);
+            bool ok = (n0 + c * 8) < N;
+            ld.b_off[j] = ok ? r * ldb * 2 + c * 16 : OOB_OFFSET;
+            ld.b_krow[j] = r;
+        } else {
+            uint32_t r = pos / (BK * 2), s = (pos % (BK * 2)) / 16;
+            uint32_t c = s ^ swz_rows<G::CHA>(r);
+            bool ok = (n0 + r) < N;
+            ld.b_off[j] = ok ? r * ldb * 2 + c * 16 : OOB_OFFSET;
+            ld.b_krow[j] = c * 8;
+        }
+    }
+
+    const uint32_t lds_base = (uint32_t)(uintptr_t)(LDS_AS uint8_t*)smem;
+    auto issue_stage = [&](uint32_t t) {
+        const uint32_t kt = t * BK;                 // k offset within the partition
+        const uint32_t st = lds_base + (t % STAGES) * G::STAGE_BYTES;
+        const bool tail = kt + BK > k_len;
+        __amdgpu_buffer_rsrc_t ra = make_rsrc(A0 + (size_t)kt * 2);
+        __amdgpu_buffer_rsrc_t rb = make_rsrc(NN ? B0 + (size_t)kt * ldb * 2 : B0 + (size_t)kt * 2);
+#pragma unroll
+        for (int j = 0; j < G::A_LOADS; j++) {
+            uint32_t off = ld.a_off[j];
+            if (tail && kt + ld.a_kchunk[j] >= k_len) off = OOB_OFFSET;
+            dma_x4(ra, __builtin_amdgcn_readfirstlane(st + (wave * G::A_LOADS + j) * 1024), off);
+        }
+#pragma unroll
+        for (int j = 0; j < G::B_LOADS; j++) {
+            uint32_t off = ld.b_off[j];
+            if (tail && kt + ld.b_krow[j] >= k_len) off = OOB_OFFSET;
+            dma_x4(rb, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + (wave * G::B_LOADS + j) * 1024), off);
+        }
+    };
+
+    f32x16_t acc[G::FM][G::FN];
+#pragma unroll
+    for (int i = 0; i < G::FM; i++)
+#pragma unroll
+        for (int j = 0; j < G::FN; j++) acc[i][j] = f32x16_t{};
+
+    // ---- per-lane operand read offsets (constant over the K loop) ------------
+    // The swizzle of every row a lane reads depends only on the lane, so each
+    // operand address is lane_base + per-kk chunk term + compile-time offset.
+    const uint32_t l32 = lane & 31, hi = lane >> 5;
+    const uint32_t a_lane = (wm * G::TM + l32) * (BK * 2);
+    const uint32_t a_swz = swz_rows<G::CHA>(l32);
+    uint32_t a_kk[BK / 16];
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; kk++) a_kk[kk] = a_lane + (((kk * 2 + hi) ^ a_swz) * 16);
+    uint32_t b_kk[BK / 16];      // NT
+    uint32_t b_col[G::FN];       // NN
+    uint32_t b_row = 0;          // NN
+    if constexpr (NN) {
+        const uint32_t g = lane >> 4, i16 = lane & 15;
+        const uint32_t s = swz_nn<G::CHB>(i16 >> 2);
+        b_row = ((g >> 1) * 8 + (i16 >> 2)) * (BN * 2);
+#pragma unroll
+        for (int j = 0; j < G::FN; j++) {
+            const uint32_t c16 = (wn * G::TN + j * 32) / 8 + (g & 1) * 2 + (i16 & 3) / 2;
+            b_col[j] = b_row + ((c16 ^ s) * 16) + (i16 & 1) * 8;
+        }
+    } else {
+        const uint32_t b_lane = (wn * G::TN + l32) * (BK * 2);
+#pragma unroll
+        for (int kk = 0; kk < BK / 16; kk++) b_kk[kk] = b_lane + (((kk * 2 + hi) ^ a_swz) * 16);
+    }
+
+    // prologue
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; s++)
+        if ((uint32_t)s < nk) issue_stage(s);
+
+    for (uint32_t t = 0; t < nk; t++) {
+        if (t + STAGES - 2 < nk) wait_vmcnt<G::LOADS * (STAGES - 2)>();
+        else wait_vmcnt<0>();
+        __syncthreads();
+        if (t + STAGES - 1 < nk) issue_stage(t + STAGES - 1);
+
+        const LDS_AS uint8_t* sa = (const LDS_AS uint8_t*)smem + (t % STAGES) * G::STAGE_BYTES;
+        const LDS_AS uint8_t* sb = sa + G::A_BYTES;
+#pragma unroll
+        for (int kk = 0; kk < BK / 16; kk++) {
+            bf16x8_t af[G::FM], bfr[G::FN];
+#pragma unroll
+            for (int i = 0; i < G::FM; i++)
+                af[i] = *(const LDS_AS bf16x8_t*)(sa + a_kk[kk] + i * 32 * (BK * 2));
+#pragma unroll
+            for (int j = 0; j < G::FN; j++) {
+                if constexpr (NN) {
+                    const LDS_AS uint8_t* p0 = sb + b_col[j] + kk * 16 * (BN * 2);
+                    bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((LDS_AS bf16x4_t*)p0);
+                    bf16x4_t hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((LDS_AS bf16x4_t*)(p0 + 4 * (BN * 2)));
+                    bfr[j] = __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
+                } else {
+                    bfr[j] = *(const LDS_AS bf16x8_t*)(sb + b_kk[kk] + j * 32 * (BK * 2));
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < G::FM; i++)
+#pragma unroll
+                for (int j = 0; j < G::FN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
+        }
+    }
+
+    // ---- epilogue -----------------------------------------------------------
+    // acc[i][j][r] holds C[m0 + wm*TM + i*32 + lane%32][n0 + wn*TN + j*32 + 8*(r/4) + 4*(lane/32) + r%4].
+    // Each 32-row block of the wave's sub-tile is staged through a
+    // wave-private LDS region [32][TN + 4] f32 and written back row-major, so
+    // global stores are full contiguous rows and the epilogue chain runs from
+    // a compact loop.
+    __syncthreads();  // all waves are done reading the stage buffers
+    float* wreg = (float*)(smem) + wave * G::EPI_WAVE_FLOATS;
+    uint8_t* Cb = (uint8_t*)p.C;
+    const bool fixup = (p.flags & T0_GEMM_FIXUP) && sk > 1;
+    const uint32_t row_base = m0 + wm * G::TM, col_base = n0 + wn * G::TN;
+
+    if (!fixup) {
+        Cb += (size_t)part * p.y_split_stride;
+#pragma unroll
+        for (int i = 0; i < G::FM; i++) {
+#pragma unroll
+            for (int j = 0; j < G::FN; j++)
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    f32x4_t v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+                    *(LDS_AS f32x4_t*)(wreg + l32 * G::EPI_LD + j * 32 + 8 * g + 4 * hi) = v;
+                }
+            emit_rowblock<G>(p, Cb, wreg, row_base + i * 32, col_base, lane);
+        }
+        return;
+    }
+
+    // Split-K fixup: every partition parks its partial tile in the workspace
+    // (register order, coalesced); the last partition to arrive sums the
+    // planes in plane order and runs the epilogue once.
+    float* ws_tile = p.workspace + ((size_t)part * tiles + tile_id) * (BM * BN);
+#pragma unroll
+    for (int i = 0; i < G::FM; i++)
+#pragma unroll
+        for (int j = 0; j < G::FN; j++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                uint32_t idx = ((i * G::FN + j) * 4 + g) * G::NT + tid;
+                f32x4_t v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+                *(f32x4_t*)(ws_tile + (size_t)idx * 4) = v;
+            }
+    __threadfence();
+    __syncthreads();
+    __shared__ uint32_t s_last;
+    if (tid == 0) {
+        uint32_t prev = atomicAdd(&p.semaphores[tile_id], 1u);
+        s_last = (prev == sk - 1) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+#pragma unroll 1
+    for (uint32_t i = 0; i < (uint32_t)G::FM; i++) {
+#pragma unroll 1
+        for (uint32_t jg = 0; jg < (uint32_t)G::FN * 4; jg++) {
+            const uint32_t j = jg / 4, g = jg % 4;
+            const uint32_t idx = (i * G::FN * 4 + jg) * G::NT + tid;
+            f32x4_t v = {0.f, 0.f, 0.f, 0.f};
+            for (uint32_t q = 0; q < sk; q++) {
+                const float* wq = p.workspace + ((size_t)q * tiles + tile_id) * (BM * BN);
+                f32x4_t w = __builtin_nontemporal_load((const f32x4_t*)(wq + (size_t)idx * 4));
+                v[0] = v[0] + w[0];
+                v[1] = v[1] + w[1];
+                v[2] = v[2] + w[2];
+                v[3] = v[3] + w[3];
+            }
+            *(LDS_AS f32x4_t*)(wreg + l32 * G::EPI_LD + j * 32 + 8 * g + 4 * hi) = v;
+        }
+        emit_rowblock<G>(p, Cb, wreg, row_base + i * 32, col_base, lane);
+    }
+    __syncthreads();
+    if (tid == 0) atomicExch(&p.semaphores[tile_id], 0u);
+}
+
+}  // namespace t0
+
+// ---------------------------------------------------------------------------
+// Instances.  Symbol: t0k_gemm_<BM>x<BN>x<BK>_w<WM>x<WN>_s<STAGES>_<nt|nn>
+// ---------------------------------------------------------------------------
+#define T0_GEMM_INSTANCE(BM, BN, BK, WM, WN, ST, NNF, TAG)                                          \
+    extern "C" __global__ void __launch_bounds__(WM * WN * 64)                                      \
+        t0k_gemm_##BM##x##BN##x##BK##_w##WM##x##WN##_s##ST##_##TAG(const t0_gemm_params p) {        \
+        t0::gemm_tile_kernel<BM, BN, BK, WM, WN, NNF, ST>(p);                                       \
+    }
+
+#define T0_GEMM_BOTH(BM, BN, BK, WM, WN, ST)          \
+    T0_GEMM_INSTANCE(BM, BN, BK, WM, WN, ST, false, nt) \
+    T0_GEMM_INSTANCE(BM, BN, BK, WM, WN, ST, true, nn)
+
+// gfx950-native tiles (auto-selection targets)
+T0_GEMM_BOTH(256, 256, 64, 2, 2, 2)
+T0_GEMM_BOTH(256, 128, 64, 2, 2, 2)
+T0_GEMM_BOTH(128, 256, 64, 2, 2, 2)
+T0_GEMM_BOTH(128, 128, 64, 2, 2, 2)
+T0_GEMM_BOTH(128, 128, 32, 2, 2, 3)
+T0_GEMM_BOTH(128, 64, 64, 2, 2, 2)
+T0_GEMM_BOTH(64, 128, 64, 2, 2, 2)
+T0_GEMM_BOTH(64, 64, 64, 1, 1, 2)
+T0_GEMM_BOTH(32, 64, 64, 1, 1, 2)
+T0_GEMM_BOTH(32, 128, 64, 1, 2, 2)
+// the reference's preset geometries (src/t0/gemm_gen.rs:86-145), wave64
+T0_GEMM_BOTH(32, 64, 16, 1, 1, 2)
+T0_GEMM_BOTH(32, 64, 32, 1, 1, 2)
+T0_GEMM_BOTH(32, 128, 16, 1, 1, 2)
+T0_GEMM_BOTH(64, 64, 16, 1, 1, 2)
+T0_GEMM_BOTH(64, 64, 32, 1, 1, 2)
+T0_GEMM_BOTH(128, 64, 16, 2, 1, 2)
+T0_GEMM_BOTH(128, 64, 32, 2, 1, 2)
+T0_GEMM_BOTH(64, 128, 16, 1, 1, 2)
+T0_GEMM_BOTH(128, 128, 16, 2, 1, 2)

@@ -1,0 +1,371 @@
+"""bf16 GEMM parity on the GPU: every gfx950 kernel instance against the CPU
+oracle (the reference's cpu_gemm_bf16 restated), through every entry point
+the reference exposes (gemm_gen dispatch, tile_ir dispatch, raw load +
+dispatch, high-level t0_gemm, tuner)."""
+import os
+import struct
+
+import numpy as np
+import pytest
+
+import t0_gpu as t0
+from gpu_util import Dev, bf16, check_close, f32, tolerance
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def rt():
+    r = t0.GpuRuntime(0)
+    yield r
+    r.close()
+
+
+@pytest.fixture()
+def dev(rt):
+    d = Dev(rt)
+    yield d
+    d.free()
+
+
+def run_gemm(rt, dev, a, b, m, n, k, layout, out_dtype, cfg=None, **kw):
+    da, db = dev.up(a), dev.up(b)
+    ob = 2 if out_dtype == t0.OUT_BF16 else 4
+    dc = dev.zeros(m * n * ob)
+    rt.gemm(da, db, dc, m, n, k, transpose=layout, out_dtype=out_dtype, cfg=cfg, **kw)
+    if out_dtype == t0.OUT_BF16:
+        return f32(dev.down(dc, np.uint16, m * n).reshape(m, n))
+    return dev.down(dc, np.float32, m * n).reshape(m, n)
+
+
+def instance_configs():
+    out = []
+    for name in t0.PRESETS:
+        c = getattr(t0.GemmConfig, name)()
+        if c.is_feasible() and c.n_col_passes == 1 and c.use_lds:
+            out.append(c)
+    return out
+
+
+# ---------------------------------------------------------- exact layouts --
+
+@pytest.mark.parametrize("layout", [t0.NT, t0.NN])
+def test_integer_pattern_exact(rt, dev, layout):
+    """Small integers: every partial sum is exact, so any MFMA operand or
+    accumulator layout mistake shows as an exact mismatch."""
+    m, n, k = 64, 96, 128
+    ai = (np.arange(m * k) % 17 - 8).reshape(m, k)          # src/t0/tile_ir.rs:5056-5057
+    bi_nt = (np.arange(n * k) % 13 - 6).reshape(n, k)
+    b = bf16(bi_nt if layout == t0.NT else bi_nt.T.copy())
+    want = ai.astype(np.int64) @ bi_nt.T.astype(np.int64)
+    for cfg in instance_configs():
+        got = run_gemm(rt, dev, bf16(ai), b, m, n, k, layout, t0.OUT_F32, cfg=cfg.copy(transpose=layout))
+        assert np.array_equal(got.astype(np.int64), want), cfg.name()
+
+
+def test_smoke_pattern_256(rt, dev):
+    """src/t0/auto_gemm.rs:235-269 smoke pattern, every instance, both layouts."""
+    s = 256
+    ai = (np.arange(s * s) % 7 - 3).reshape(s, s)
+    bi = (np.arange(s * s) % 5 - 2).reshape(s, s)          # WT[N,K]
+    want = ai.astype(np.int64) @ bi.T.astype(np.int64)
+    for cfg in instance_configs():
+        for layout, b in ((t0.NT, bf16(bi)), (t0.NN, bf16(bi.T.copy()))):
+            got = run_gemm(rt, dev, bf16(ai), b, s, s, s, layout, t0.OUT_F32, cfg=cfg.copy(transpose=layout))
+            assert np.array_equal(got.astype(np.int64), want), (cfg.name(), layout)
+
+
+# ------------------------------------------------------- correctness matrix --
+
+SIZES = [(64, 64, 64), (128, 128, 128), (256, 256, 256), (64, 256, 64), (128, 1024, 256), (256, 512, 512)]
+
+
+@pytest.mark.parametrize("m,k,n", SIZES)
+def test_gemm_correctness_matrix(rt, dev, m, k, n):
+    """examples/test_gemm_correctness.rs:66-86: xorshift U(-1,1) bf16 data,
+    seeds m*1000+k and n*2000+k; all instances x {NT,NN} x {f32,bf16}."""
+    x = orc.xorshift_bf16(m * k, m * 1000 + k).reshape(m, k)
+    wt = orc.xorshift_bf16(n * k, n * 2000 + k).reshape(n, k)
+    ref = orc.gemm_nt(x, wt)
+    tol = tolerance(f32(x), f32(wt), k)
+    for cfg in instance_configs():
+        for layout, b in ((t0.NT, wt), (t0.NN, wt.T.copy())):
+            for od in (t0.OUT_F32, t0.OUT_BF16):
+                got = run_gemm(rt, dev, x, b, m, n, k, layout, od, cfg=cfg.copy(transpose=layout, out_dtype=od))
+                check_close(got, ref, tol, f"{cfg.name()} layout={layout} out={od}")
+                if od == t0.OUT_F32:
+                    # f32 accumulation order differs from the sequential loop only by rounding
+                    assert np.max(np.abs(got - ref)) <= 2e-5 * k
+
+
+def test_bf16_output_is_rne_of_f32(rt, dev):
+    m = n = k = 512
+    rng = np.random.default_rng(5)
+    a = bf16(rng.standard_normal((m, k)))
+    b = bf16(rng.standard_normal((k, n)))
+    cfg = t0.GemmConfig.tile_128x128_k64()
+    g32 = run_gemm(rt, dev, a, b, m, n, k, t0.NN, t0.OUT_F32, cfg=cfg.copy(transpose=t0.NN))
+    g16 = run_gemm(rt, dev, a, b, m, n, k, t0.NN, t0.OUT_BF16, cfg=cfg.copy(transpose=t0.NN, out_dtype=t0.OUT_BF16))
+    assert np.array_equal(f32(orc.bf16_rne(g32)).view(np.uint32), g16.view(np.uint32))
+
+
+# ---------------------------------------------------------- golden vectors --
+
+def _golden(golden_dir, name, dtype, shape):
+    return np.fromfile(os.path.join(golden_dir, name), dtype=dtype).reshape(shape)
+
+
+def test_torch_fixture_gemm(rt, dev, golden_dir):
+    """benchmarks/torch_ref (seed 42): X[64,256] . W_gate[512,256]^T."""
+    x = _golden(golden_dir, "x.bin", np.uint16, (64, 256))
+    w = _golden(golden_dir, "w_gate.bin", np.uint16, (512, 256))
+    ref32 = _golden(golden_dir, "h_gate_f32ref.bin", np.float32, (64, 512))
+    ref16 = _golden(golden_dir, "h_gate_bf16acc.bin", np.float32, (64, 512))
+    tol = tolerance(f32(x), f32(w), 256)
+    for cfg in (None, t0.GemmConfig.tile_64x64_k64(), t0.GemmConfig.tile_256x256_k64()):
+        got = run_gemm(rt, dev, x, w, 64, 512, 256, t0.NT, t0.OUT_F32, cfg=cfg)
+        check_close(got, ref32, tol, "h_gate f32")
+        assert np.max(np.abs(got - ref32)) < 5e-6
+        g16 = run_gemm(rt, dev, x, w, 64, 512, 256, t0.NT, t0.OUT_BF16,
+                       cfg=cfg.copy(out_dtype=t0.OUT_BF16) if cfg is not None else None)
+        assert np.mean(g16 == ref16) > 0.99
+        assert np.all(np.abs(g16 - ref16) <= np.abs(ref16) * 2.0**-7 + 1e-30)
+
+
+def test_torch_fixture_second_gemm(rt, dev, golden_dir):
+    s = _golden(golden_dir, "swiglu_bf16_trunc.bin", np.uint16, (64, 512))
+    wd = _golden(golden_dir, "w_down.bin", np.uint16, (256, 512))
+    ref = _golden(golden_dir, "y_bf16_f32acc.bin", np.float32, (64, 256))
+    got = run_gemm(rt, dev, s, wd, 64, 256, 512, t0.NT, t0.OUT_F32)
+    check_close(got, ref, tolerance(f32(s), f32(wd), 512), "y")
+    # same product in NN form
+    got_nn = run_gemm(rt, dev, s, wd.T.copy(), 64, 256, 512, t0.NN, t0.OUT_F32)
+    check_close(got_nn, ref, tolerance(f32(s), f32(wd), 512), "y nn")
+
+
+# ----------------------------------------------------------------- bounds --
+
+@pytest.mark.parametrize("m,n,k", [(33, 31, 40), (1, 1, 8), (255, 257, 264), (100, 200, 72), (300, 130, 1000)])
+def test_boundary_sentinel(rt, dev, m, n, k):
+    """src/t0/tile_boundary_tests.rs: rows/cols outside M x N stay untouched
+    (sentinel -9999 in a padded C with ldc > N), everything inside matches."""
+    rng = np.random.default_rng(m * 7 + n)
+    a = bf16(rng.uniform(-1, 1, (m, k)))
+    b = bf16(rng.uniform(-1, 1, (k, n)))
+    ref = orc.gemm_nn(a, b)
+    ldc = n + 12
+    for cfg in (t0.GemmConfig.tile_256x256_k64(), t0.GemmConfig.tile_128x64_k16(), t0.GemmConfig.tile_32x64_k64(),
+                t0.GemmConfig.tile_128x128_k32()):
+        for layout, bb in ((t0.NN, b), (t0.NT, b.T.copy())):
+            c = np.full((m + 3, ldc), -9999.0, np.float32)
+            dc = dev.up(c)
+            rt.gemm(dev.up(a), dev.up(bb), dc, m, n, k, transpose=layout, cfg=cfg.copy(transpose=layout), ldc=ldc)
+            out = dev.down(dc, np.float32, c.size).reshape(c.shape)
+            check_close(out[:m, :n], ref, tolerance(f32(a), f32(b), k), f"{cfg.name()} {layout}")
+            assert np.all(out[:m, n:] == -9999.0) and np.all(out[m:, :] == -9999.0), cfg.name()
+
+
+def test_generic_fallback_unaligned(rt, dev):
+    """K % 8 != 0 and an odd lda: the generic kernel takes it."""
+    m, n, k = 37, 45, 37
+    rng = np.random.default_rng(3)
+    a = bf16(rng.uniform(-1, 1, (m, k + 3)))                 # lda = k + 3
+    b = bf16(rng.uniform(-1, 1, (n, k)))
+    ref = orc.gemm_nt(a[:, :k].copy(), b)
+    da, db = dev.up(a), dev.up(b)
+    dc = dev.zeros(m * n * 4)
+    rt.gemm(da, db, dc, m, n, k, transpose=t0.NT, lda=k + 3)
+    got = dev.down(dc, np.float32, m * n).reshape(m, n)
+    check_close(got, ref, tolerance(f32(a), f32(b), k), "generic")
+
+
+# --------------------------------------------------- reference entry points --
+
+def test_gemm_gen_dispatch_path(rt, dev):
+    """ensure_kernel_t0 + build_kernargs (40 B) + compute_grid_auto + dispatch,
+    as examples/hello_gemm_gen.rs does, including split-K planes summed on the
+    host and the 48-byte bias+ReLU variant."""
+    m, n, k = 256, 192, 512
+    x = orc.xorshift_bf16(m * k, 11).reshape(m, k)
+    wt = orc.xorshift_bf16(n * k, 12).reshape(n, k)
+    ref = orc.gemm_nt(x, wt)
+    tol = tolerance(f32(x), f32(wt), k)
+    dx, dw = dev.up(x), dev.up(wt)
+    for cfg in (t0.GemmConfig.tile_128x64_k16(), t0.GemmConfig.tile_64x64_k32().copy(split_k=4),
+                t0.GemmConfig.tile_32x64_k16().copy(split_k=2, swap_grid=0)):
+        sk = max(1, cfg.split_k)
+        kern = rt.ensure_kernel_t0(cfg)
+        assert kern.info()["kernarg_size"] == 40
+        dy = dev.zeros(m * n * 4 * sk)
+        gx, gy = t0.compute_grid_auto(cfg, m, n)
+        rt.dispatch(kern, [gx, gy, 1], t0.build_kernargs(dx, dw, dy, k, n, m, cfg))
+        planes = dev.down(dy, np.float32, m * n * sk).reshape(sk, m, n)
+        got = orc.splitk_sum(planes)
+        check_close(got, ref, tol, cfg.name())
+    bias = np.linspace(-1, 1, n).astype(np.float32)
+    cfg = t0.GemmConfig.tile_64x64_k16().copy(epilogue=t0.EPI_BIAS_ADD_RELU)
+    kern = rt.ensure_kernel_t0(cfg)
+    dy = dev.zeros(m * n * 4)
+    gx, gy = t0.compute_grid_auto(cfg, m, n)
+    rt.dispatch(kern, [gx, gy, 1], t0.build_kernargs_with_bias(dx, dw, dy, k, n, m, cfg, dev.up(bias)))
+    got = dev.down(dy, np.float32, m * n).reshape(m, n)
+    check_close(got, np.maximum(ref + bias, 0), tol, "bias_relu")
+
+
+def _epi_ref(y, ops, bias, scale, lo, hi):
+    y = y.astype(np.float64)
+    for op in ops:
+        if op == "bias": y = y + bias
+        elif op == "scale": y = y * scale
+        elif op == "relu": y = np.maximum(y, 0)
+        elif op == "silu": y = y / (1 + np.exp(-y))
+        elif op == "gelu": y = y / (1 + np.exp(-1.702 * y))
+        elif op == "abs": y = np.abs(y)
+        elif op == "neg": y = -y
+        elif op == "clamp": y = np.clip(y, lo, hi)
+    return y
+
+
+@pytest.mark.parametrize("ops", [["bias", "silu"], ["scale", "gelu"], ["neg", "abs", "clamp"], ["bias", "relu", "scale"]])
+def test_tile_ir_dispatch_epilogues(rt, dev, ops):
+    """TileGemm + build_kernargs_m (44 B + epilogue args) + dispatch, epilogue
+    chain semantics of src/t0/tile_ir.rs:3406-3540 (GELU = x*sigmoid(1.702x))."""
+    m, n, k = 192, 256, 320
+    rng = np.random.default_rng(len(ops))
+    x = bf16(rng.uniform(-1, 1, (m, k)))
+    wt = bf16(rng.uniform(-1, 1, (n, k)))
+    bias = rng.uniform(-2, 2, n).astype(np.float32)
+    ref = _epi_ref(orc.gemm_nt(x, wt), ops, bias, 0.75, -0.5, 1.5)
+    spec = t0.TileGemm.make(128, 128, 64, epilogue=ops)
+    kern = rt.ensure_tile_kernel(spec)
+    dy = dev.zeros(m * n * 4)
+    ka = spec.build_kernargs_m(dev.up(x), dev.up(wt), dy, k, n, m, bias=dev.up(bias), scale=0.75, clamp_min=-0.5,
+                               clamp_max=1.5)
+    assert len(ka) == kern.info()["kernarg_size"]
+    rt.dispatch(kern, spec.compute_grid(m, n), ka)
+    got = dev.down(dy, np.float32, m * n).reshape(m, n)
+    check_close(got, ref, tolerance(f32(x), f32(wt), k) * 2, "+".join(ops))
+
+
+def test_fixup_split_k_bf16_deterministic(rt, dev):
+    """split-K reduced in-kernel (bf16 output, epilogue once), twice, bitwise equal."""
+    m, n, k = 128, 512, 4096
+    rng = np.random.default_rng(8)
+    a = bf16(rng.standard_normal((m, k)) * 0.5)
+    b = bf16(rng.standard_normal((k, n)) * 0.5)
+    ref = orc.gemm_nn(a, b)
+    for sk in (2, 4, 8):
+        cfg = t0.GemmConfig.tile_128x128_k64().copy(split_k=sk, transpose=t0.NN, out_dtype=t0.OUT_BF16)
+        g1 = run_gemm(rt, dev, a, b, m, n, k, t0.NN, t0.OUT_BF16, cfg=cfg)
+        g2 = run_gemm(rt, dev, a, b, m, n, k, t0.NN, t0.OUT_BF16, cfg=cfg)
+        assert np.array_equal(g1.view(np.uint32), g2.view(np.uint32))
+        check_close(g1, ref, tolerance(f32(a), f32(b), k), f"sk={sk}")
+
+
+def test_raw_kernel_load_and_dispatch(rt, dev):
+    """GpuKernel::load of the library's code object + raw kernarg dispatch."""
+    n = 4096
+    x = np.random.default_rng(2).standard_normal(n).astype(np.float32) * 100
+    src, dst = dev.up(x), dev.zeros(n * 2)
+    kern = rt.kernel_load(t0.code_object(), "t0k_f32_to_bf16", [256], kernarg_size=48)
+    # t0_aux_params: src, dst, m, n, ld_src, ld_dst, planes, flags, plane_stride
+    ka = struct.pack("<QQIIIIIIQ", src, dst, 1, n, n, n, 0, 0, 0)
+    rt.dispatch(kern, [n, 1, 1], ka)
+    got = dev.down(dst, np.uint16, n)
+    assert np.array_equal(got, orc.bf16_rne(x))
+
+
+def test_poisoned_runtime_refuses_dispatch(dev):
+    """src/ignis/gpu_context.rs:311-313: a poisoned runtime fails fast."""
+    with t0.GpuRuntime(0) as r2:
+        cfg = t0.GemmConfig.tile_64x64_k16()
+        kern = r2.ensure_kernel_t0(cfg)
+        r2.mark_poisoned()
+        assert r2.is_poisoned()
+        with pytest.raises(t0.T0Error) as e:
+            r2.dispatch(kern, [64, 1, 1], bytes(40))
+        assert e.value.status == -4
+
+
+def test_kernarg_length_mismatch_rejected(rt):
+    """src/ignis/gpu_context.rs:319-322."""
+    kern = rt.ensure_kernel_t0(t0.GemmConfig.tile_64x64_k16())
+    with pytest.raises(t0.T0Error) as e:
+        rt.dispatch(kern, [64, 1, 1], bytes(44))
+    assert e.value.status == -5
+
+
+# ------------------------------------------------------------ small kernels --
+
+def test_splitk_reduce_f32_to_bf16_unpad(rt, dev):
+    rng = np.random.default_rng(4)
+    planes = rng.standard_normal((4, 65, 130)).astype(np.float32)
+    dp = dev.up(planes)
+    do = dev.zeros(65 * 130 * 4)
+    rt.splitk_reduce(dp, 65 * 130 * 4, 4, do, 65, 130)
+    assert np.array_equal(dev.down(do, np.float32, 65 * 130).reshape(65, 130), orc.splitk_sum(planes))
+    dob = dev.zeros(65 * 130 * 2)
+    rt.splitk_reduce(dp, 65 * 130 * 4, 4, dob, 65, 130, out_bf16=True)
+    assert np.array_equal(dev.down(dob, np.uint16, 65 * 130).reshape(65, 130), orc.bf16_rne(orc.splitk_sum(planes)))
+    padded = rng.standard_normal((33, 96)).astype(np.float32)
+    dpad, dout = dev.up(padded), dev.zeros(33 * 70 * 4)
+    rt.unpad_2d(dpad, dout, 33, 70, 96)
+    assert np.array_equal(dev.down(dout, np.float32, 33 * 70).reshape(33, 70), padded[:, :70])
+
+
+# ----------------------------------------------------- headline-size checks --
+
+def _sampled_rows(m, count=16):
+    return sorted(set(np.linspace(0, m - 1, count).astype(int).tolist()))
+
+
+def test_headline_4096_nn_bf16(rt, dev):
+    """4096^3 NN, N(0,1) bf16 inputs, bf16 output; sampled
+    rows against the oracle (full oracle is 137 GFLOP), plus the chosen
+    kernel against a second kernel on the whole matrix."""
+    m = n = k = 4096
+    rng = np.random.default_rng(42)
+    a = bf16(rng.standard_normal((m, k)))
+    b = bf16(rng.standard_normal((k, n)))
+    got = run_gemm(rt, dev, a, b, m, n, k, t0.NN, t0.OUT_BF16)
+    rows = _sampled_rows(m)
+    ref = np.stack([orc.gemm_rows(a, b, "nn", r, r + 1)[0] for r in rows])
+    check_close(got[rows], ref, tolerance(f32(a), f32(b), k), "4096^3")
+    other = run_gemm(rt, dev, a, b, m, n, k, t0.NN, t0.OUT_BF16,
+                     cfg=t0.GemmConfig.tile_128x128_k64().copy(transpose=t0.NN, out_dtype=t0.OUT_BF16))
+    check_close(got, other, tolerance(f32(a), f32(b), k), "4096^3 vs 128x128")
+
+
+def test_skinny_128x4096x4096(rt, dev):
+    """M=128, N=K=4096, N(0,0.02) inputs, bf16 out."""
+    m, n, k = 128, 4096, 4096
+    rng = np.random.default_rng(43)
+    a = bf16(rng.normal(0, 0.02, (m, k)))
+    b = bf16(rng.normal(0, 0.02, (k, n)))
+    got = run_gemm(rt, dev, a, b, m, n, k, t0.NN, t0.OUT_BF16)
+    rows = _sampled_rows(m, 12)
+    ref = np.stack([orc.gemm_rows(a, b, "nn", r, r + 1)[0] for r in rows])
+    check_close(got[rows], ref, tolerance(f32(a), f32(b), k), "skinny")
+
+
+# ------------------------------------------------------------------ tuner --
+
+def test_tuner_and_auto_gemm(rt, dev, tmp_path):
+    """src/t0/auto_gemm.rs:82-216, :555-590: tune, JSON cache, cached re-tune,
+    auto_gemm result."""
+    tuner = t0.GemmTuner(cache_dir=str(tmp_path), max_candidates=4, n_iters=3)
+    cfg, tf = tuner.tune(rt, 512, 512, 512)
+    assert cfg.is_feasible() or cfg.split_k > 1
+    assert tf > 0
+    files = list(tmp_path.glob("gemm_gfx950_512x512x512_nt_f32.json"))
+    assert files, list(tmp_path.iterdir())
+    cfg2, tf2 = tuner.tune(rt, 512, 512, 512)
+    assert cfg2.name() == cfg.name() and tf2 == tf
+    m = n = k = 512
+    x = orc.xorshift_bf16(m * k, 1).reshape(m, k)
+    wt = orc.xorshift_bf16(n * k, 2).reshape(n, k)
+    dc = dev.zeros(m * n * 4)
+    t0.auto_gemm(rt, dev.up(x), dev.up(wt), dc, m, n, k)
+    check_close(dev.down(dc, np.float32, m * n).reshape(m, n), orc.gemm_nt(x, wt), tolerance(f32(x), f32(wt), k),
+                "auto_gemm")

@@ -287,7 +287,7 @@ def test_w4a16_integer_closed_form():
     qw = orc.int4_pack(q.reshape(-1)).view("<u4").reshape(n, k // 8)
     ai = rng.integers(-4, 5, size=(m, k))
     a = _bf16_of_ints(ai)
-    scales = np.full((n, k // gs), 0x3F80, np.uint16)
+    scales = np.full((k // gs, n), 0x3F80, np.uint16)
     y = orc.w4a16(a, qw, scales, None, 8, m, n, k, gs)
     want = ai.astype(np.int64) @ (q.astype(np.int64) - 8).T
     assert np.array_equal(y.astype(np.int64), want)
@@ -299,16 +299,18 @@ def test_w4a16_per_group_zeros_and_scales():
     G = k // gs
     q = rng.integers(0, 16, size=(n, k), dtype=np.uint8)
     qw = orc.int4_pack(q.reshape(-1)).view("<u4").reshape(n, k // 8)
-    z = rng.integers(0, 16, size=(n, G), dtype=np.uint8)
-    zw = np.zeros((n, (G + 7) // 8), np.uint32)
-    for g in range(G):
-        zw[:, g // 8] |= z[:, g].astype(np.uint32) << (4 * (g % 8))
-    s = orc.bf16_rne(rng.uniform(0.005, 0.02, size=(n, G)).astype(np.float32))
+    z = rng.integers(0, 16, size=(G, n), dtype=np.uint8)      # [G][N]
+    zw = np.zeros((G, n // 8), np.uint32)                       # [G][N/8] packed
+    for j in range(n):
+        zw[:, j // 8] |= z[:, j].astype(np.uint32) << (4 * (j % 8))
+    s = orc.bf16_rne(rng.uniform(0.005, 0.02, size=(G, n)).astype(np.float32))   # [G][N]
     a = orc.bf16_rne(rng.standard_normal((m, k)).astype(np.float32))
     w = orc.w4a16_dequant(qw, s, zw, 0, n, k, gs)
     # dequant equals the GPTQ-format dequant on the same data
     packed = orc.int4_pack(q.reshape(-1))
-    w2 = orc.dequant_int4_f32(packed, orc.bf16_to_f32(s).reshape(-1), z.astype(np.int32).reshape(-1), n, k, gs)
+    # the GPTQ-format path takes [row=n][group] scales / zero points
+    w2 = orc.dequant_int4_f32(packed, orc.bf16_to_f32(s).T.copy().reshape(-1),
+                              z.T.astype(np.int32).copy().reshape(-1), n, k, gs)
     assert np.array_equal(w.view(np.uint32), w2.view(np.uint32))
     y = orc.w4a16(a, qw, s, zw, 0, m, n, k, gs)
     exact = orc.bf16_to_f32(a).astype(np.float64) @ w.astype(np.float64).T
