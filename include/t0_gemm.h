@@ -78,7 +78,7 @@ typedef enum t0_preset {
     /* gfx950-native */
     T0_PRESET_256x256_K64, T0_PRESET_256x128_K64, T0_PRESET_128x256_K64, T0_PRESET_128x128_K64,
     T0_PRESET_128x128_K32, T0_PRESET_128x64_K64, T0_PRESET_64x128_K64, T0_PRESET_32x64_K64,
-    T0_PRESET_32x128_K64,
+    T0_PRESET_32x128_K64, T0_PRESET_256x256_K32,
     T0_PRESET_COUNT
 } t0_preset;
 
@@ -264,6 +264,17 @@ int t0_event_record(t0_runtime* rt, t0_event* ev);
 int t0_event_synchronize(t0_event* ev);
 int t0_event_elapsed_ms(const t0_event* start, const t0_event* stop, float* ms);
 
+/* Stream capture into a HIP graph (no counterpart in the reference, whose
+ * DispatchQueue batches AQL packets, src/t0/prefill_dispatch.rs:61-130):
+ * everything launched on the runtime's stream between begin and end is
+ * recorded, then replayed with one launch.  Workspaces must already exist
+ * (run the same calls once before capturing). */
+typedef struct t0_graph t0_graph;
+int t0_graph_begin(t0_runtime* rt);
+int t0_graph_end(t0_runtime* rt, t0_graph** out);
+int t0_graph_launch(t0_runtime* rt, const t0_graph* g);
+int t0_graph_destroy(t0_graph* g);
+
 /* ------------------------------------------------------ high-level GEMM */
 /* One GEMM through the tuned kernel family, the way auto_gemm
  * (src/t0/auto_gemm.rs:555-590) runs one: C = epilogue(A . B).
@@ -349,6 +360,9 @@ int t0_splitk_reduce(t0_runtime* rt, uint64_t src, uint64_t plane_stride, uint32
                      uint32_t m, uint32_t n, int out_bf16);
 /* f32 -> bf16 RNE (src/ignis/ops/bf16_matmul.rs:356-383 does this on the CPU). */
 int t0_f32_to_bf16(t0_runtime* rt, uint64_t src, uint64_t dst, uint64_t count);
+/* Device-to-device copy through a plain 16-byte-per-lane kernel (no
+ * counterpart in the reference): the calibration kernel for HBM byte counters. */
+int t0_copy_device(t0_runtime* rt, uint64_t src, uint64_t dst, uint64_t bytes);
 /* t0_unpad_2d (src/t0/math.rs): out[m][n] = padded[m][n_pad]. */
 int t0_unpad_2d(t0_runtime* rt, uint64_t padded, uint64_t out, uint32_t m, uint32_t n, uint32_t n_pad);
 

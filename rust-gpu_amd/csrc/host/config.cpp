@@ -31,13 +31,12 @@ const char* last_error() { return g_last_error.c_str(); }
 // Must list exactly the T0_GEMM_BOTH(...) instances of gemm_bf16.hip.
 const std::vector<GemmInstance>& gemm_instances() {
     static const std::vector<GemmInstance> v = {
-        {256, 256, 64, 2, 2, 2}, {256, 128, 64, 2, 2, 2}, {128, 256, 64, 2, 2, 2},
-        {128, 128, 64, 2, 2, 2}, {128, 128, 32, 2, 2, 3}, {128, 64, 64, 2, 2, 2},
-        {64, 128, 64, 2, 2, 2},  {64, 64, 64, 1, 1, 2},   {32, 64, 64, 1, 1, 2},
-        {32, 128, 64, 1, 2, 2},
-        {32, 64, 16, 1, 1, 2},   {32, 64, 32, 1, 1, 2},   {32, 128, 16, 1, 1, 2},
-        {64, 64, 16, 1, 1, 2},   {64, 64, 32, 1, 1, 2},   {128, 64, 16, 2, 1, 2},
-        {128, 64, 32, 2, 1, 2},  {64, 128, 16, 1, 1, 2},  {128, 128, 16, 2, 1, 2},
+        {256, 256, 64, 2, 2, 2}, {256, 256, 32, 2, 2, 4}, {256, 128, 64, 2, 2, 3}, {128, 256, 64, 2, 2, 3},
+        {128, 128, 64, 2, 2, 4}, {128, 128, 32, 2, 2, 4}, {128, 64, 64, 2, 2, 4},  {64, 128, 64, 2, 2, 4},
+        {64, 64, 64, 1, 1, 4},   {32, 64, 64, 1, 1, 6},   {32, 128, 64, 1, 2, 4},
+        {32, 64, 16, 1, 1, 4},   {32, 64, 32, 1, 1, 4},   {32, 128, 16, 1, 1, 4},
+        {64, 64, 16, 1, 1, 4},   {64, 64, 32, 1, 1, 4},   {128, 64, 16, 2, 1, 4},
+        {128, 64, 32, 2, 1, 4},  {64, 128, 16, 1, 1, 4},  {128, 128, 16, 2, 1, 4},
     };
     return v;
 }
@@ -135,6 +134,7 @@ static bool preset(int id, t0_gemm_config* o) {
     case T0_PRESET_64x128_K64: *o = mk(64, 128, 64, 256, true, true, 1, false); return true;
     case T0_PRESET_32x64_K64: *o = mk(32, 64, 64, 64, true, true, 1, false); return true;
     case T0_PRESET_32x128_K64: *o = mk(32, 128, 64, 128, true, true, 1, false); return true;
+    case T0_PRESET_256x256_K32: *o = mk(256, 256, 32, 256, true, true, 1, false); return true;
     default: return false;
     }
 }
@@ -362,7 +362,7 @@ int t0_sweep_configs(t0_gemm_config* out, size_t cap) {
                        T0_PRESET_64x64_K16, T0_PRESET_64x64_K32, T0_PRESET_128x64_K16, T0_PRESET_64x128_K16,
                        T0_PRESET_128x64_K32, T0_PRESET_256x256_K64, T0_PRESET_256x128_K64, T0_PRESET_128x256_K64,
                        T0_PRESET_128x128_K64, T0_PRESET_128x128_K32, T0_PRESET_128x64_K64, T0_PRESET_64x128_K64,
-                       T0_PRESET_32x64_K64, T0_PRESET_32x128_K64};
+                       T0_PRESET_32x64_K64, T0_PRESET_32x128_K64, T0_PRESET_256x256_K32};
     for (int id : ids) { t0_gemm_config c; preset(id, &c); v.push_back(c); }
     return fill_list(v, out, cap);
 }

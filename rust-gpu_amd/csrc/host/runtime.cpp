@@ -643,6 +643,50 @@ int t0_event_elapsed_ms(const t0_event* a, const t0_event* b, float* ms) {
     return T0_OK;
 }
 
+// ----------------------------------------------------------------- graphs --
+struct t0_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+int t0_graph_begin(t0_runtime* rt) {
+    if (!rt) return fail(T0_ERR_INVALID, "null runtime");
+    int r = set_dev(rt);
+    if (r) return r;
+    HIPCHK(hipStreamBeginCapture(rt->stream, hipStreamCaptureModeThreadLocal));
+    return T0_OK;
+}
+
+int t0_graph_end(t0_runtime* rt, t0_graph** out) {
+    if (!rt || !out) return fail(T0_ERR_INVALID, "null argument");
+    auto* g = new t0_graph();
+    hipError_t e = hipStreamEndCapture(rt->stream, &g->graph);
+    if (e != hipSuccess) { delete g; return fail(T0_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(e)); }
+    e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        hipGraphDestroy(g->graph);
+        delete g;
+        return fail(T0_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
+    }
+    *out = g;
+    return T0_OK;
+}
+
+int t0_graph_launch(t0_runtime* rt, const t0_graph* g) {
+    if (!rt || !g) return fail(T0_ERR_INVALID, "null argument");
+    if (rt->poisoned.load()) return fail(T0_ERR_POISONED, "runtime poisoned; refusing graph launch");
+    HIPCHK(hipGraphLaunch(g->exec, rt->stream));
+    return T0_OK;
+}
+
+int t0_graph_destroy(t0_graph* g) {
+    if (!g) return T0_OK;
+    if (g->exec) hipGraphExecDestroy(g->exec);
+    if (g->graph) hipGraphDestroy(g->graph);
+    delete g;
+    return T0_OK;
+}
+
 // ------------------------------------------------------------ high level --
 static int desc_to_params(const t0_gemm_desc* d, const t0_gemm_config& c, t0_gemm_params& p) {
     memset(&p, 0, sizeof p);
@@ -990,15 +1034,17 @@ static int w4_plan(t0_runtime* rt, const t0_w4a16_desc* d, W4Plan& pl) {
         const uint32_t mb = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
         const uint32_t waves = (mb == 1 && N % 128 == 0) ? 8 : 4;
         const uint32_t ncw = 16 * waves;
+        const uint32_t kc_max = 1024 / mb;   // the kernel's K slice limit (LDS staging)
         uint32_t sk = d->split_k;
         if (!sk) {
-            // enough workgroups to cover the CUs a few times; slice <= 1024
+            // enough workgroups to cover the CUs a few times within the slice limit
             sk = 1;
-            while (sk < 16 && ((uint64_t)(N / ncw) * sk < 512 || K / sk > 1024) && (K / (2 * sk)) % 128 == 0 &&
+            while (sk < 16 && ((uint64_t)(N / ncw) * sk < 512 || K / sk > kc_max) && (K / (2 * sk)) % 128 == 0 &&
                    K / (2 * sk) >= 128)
                 sk *= 2;
         }
-        if (K % (128 * sk) || K / sk > 1024) return fail(T0_ERR_INVALID, "split_k %u does not fit K %u", sk, K);
+        if (K % (128 * sk) || K / sk > kc_max)
+            return fail(T0_ERR_INVALID, "split_k %u does not fit K %u (slice <= %u)", sk, K, kc_max);
         char b[64];
         snprintf(b, sizeof b, "t0k_w4a16_decode_w%u_mb%u", waves, mb);
         pl.sym = b;
@@ -1119,6 +1165,20 @@ int t0_f32_to_bf16(t0_runtime* rt, uint64_t src, uint64_t dst, uint64_t count) {
     p.src = (const void*)src; p.dst = (void*)dst;
     p.m = 1; p.n = (uint32_t)count; p.ld_src = p.n; p.ld_dst = p.n;
     return launch(rt, f, (uint32_t)((count + 255) / 256), 1, 1, 256, p);
+}
+
+int t0_copy_device(t0_runtime* rt, uint64_t src, uint64_t dst, uint64_t bytes) {
+    if (!rt || !src || !dst || bytes % 16 || (src | dst) % 16) return fail(T0_ERR_INVALID, "16-byte aligned copy only");
+    int r = set_dev(rt);
+    if (r) return r;
+    hipFunction_t f;
+    r = get_fn(rt, "t0k_copy_b128", &f);
+    if (r) return r;
+    t0_aux_params p;
+    memset(&p, 0, sizeof p);
+    p.src = (const void*)src; p.dst = (void*)dst;
+    p.plane_stride = bytes / 16;
+    return launch(rt, f, (uint32_t)((bytes / 16 + 255) / 256), 1, 1, 256, p);
 }
 
 int t0_unpad_2d(t0_runtime* rt, uint64_t padded, uint64_t out, uint32_t m, uint32_t n, uint32_t n_pad) {

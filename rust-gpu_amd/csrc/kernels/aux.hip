@@ -97,3 +97,10 @@ extern "C" __global__ void __launch_bounds__(256) t0k_gemm_generic_nn(const t0_g
 extern "C" __global__ void __launch_bounds__(256) t0k_splitk_reduce(const t0_aux_params p) { t0::splitk_reduce(p); }
 extern "C" __global__ void __launch_bounds__(256) t0k_f32_to_bf16(const t0_aux_params p) { t0::f32_to_bf16(p); }
 extern "C" __global__ void __launch_bounds__(256) t0_unpad_2d(const t0_aux_params p) { t0::unpad_2d(p); }
+
+// Plain 16-byte-per-lane copy of n16 chunks: the calibration kernel whose
+// known byte count scales the FETCH_SIZE / WRITE_SIZE counters.
+extern "C" __global__ void __launch_bounds__(256) t0k_copy_b128(const t0_aux_params p) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < p.plane_stride) ((u32x4_t*)p.dst)[i] = ((const u32x4_t*)p.src)[i];
+}

@@ -79,6 +79,35 @@ T0_DEV bool epi_has_bias(uint32_t ops) {
     return false;
 }
 
+// ------------------------------------------------- cross-workgroup partials --
+// Split-K partial sums move between workgroups (possibly on different XCDs,
+// each with its own L2) through agent-scope relaxed atomic stores/loads:
+// these bypass the non-coherent L2, so no cache-wide writeback/invalidate
+// (what a device-scope fence costs) is needed.  Protocol: each workgroup
+// stores its partials with st_agent, waits for its stores (publish()), then
+// bumps a counter; the workgroup that sees the last count reads every
+// partial with ld_agent.
+T0_DEV void st_agent(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+T0_DEV float ld_agent(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// all of this workgroup's stores are performed, then the counter is bumped by
+// one lane; returns true in every thread of the workgroup that arrived last.
+T0_DEV bool publish_and_count(uint32_t* counter, uint32_t total, uint32_t* lds_flag) {
+    __builtin_amdgcn_s_waitcnt(0);   // vmcnt(0): this thread's stores are done
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *lds_flag = (prev == total - 1) ? 1u : 0u;
+    }
+    __syncthreads();
+    return *lds_flag != 0;
+}
+T0_DEV void reset_counter(uint32_t* counter) {
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ------------------------------------------------------------- tile order --
 // Workgroups are dispatched round-robin over the 8 XCDs (workgroup b runs on
 // XCD b % 8).  Remap so that consecutive logical ids share an XCD (and its

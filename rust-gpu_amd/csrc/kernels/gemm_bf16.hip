@@ -272,9 +272,9 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
 
         const LDS_AS uint8_t* sa = (const LDS_AS uint8_t*)smem + (t % STAGES) * G::STAGE_BYTES;
         const LDS_AS uint8_t* sb = sa + G::A_BYTES;
-#pragma unroll
-        for (int kk = 0; kk < BK / 16; kk++) {
-            bf16x8_t af[G::FM], bfr[G::FN];
+        // operand fragments of one 16-deep k step, double-buffered in
+        // registers: step kk+1 is read from LDS while step kk's MFMAs run
+        auto load_frags = [&](int kk, bf16x8_t* af, bf16x8_t* bfr) {
 #pragma unroll
             for (int i = 0; i < G::FM; i++)
                 af[i] = *(const LDS_AS bf16x8_t*)(sa + a_kk[kk] + i * 32 * (BK * 2));
@@ -289,11 +289,21 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
                     bfr[j] = *(const LDS_AS bf16x8_t*)(sb + b_kk[kk] + j * 32 * (BK * 2));
                 }
             }
+        };
+        bf16x8_t af[2][G::FM], bfr[2][G::FN];
+        load_frags(0, af[0], bfr[0]);
+#pragma unroll
+        for (int kk = 0; kk < BK / 16; kk++) {
+            const int cur = kk & 1;
+            if (kk + 1 < BK / 16) load_frags(kk + 1, af[cur ^ 1], bfr[cur ^ 1]);
+            // keep the next step's LDS reads ahead of this step's MFMAs (the
+            // scheduler would otherwise sink them next to their uses)
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < G::FM; i++)
 #pragma unroll
                 for (int j = 0; j < G::FN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[cur][j], af[cur][i], acc[i][j], 0, 0, 0);
         }
     }
 
@@ -336,19 +346,11 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
 #pragma unroll
             for (int g = 0; g < 4; g++) {
                 uint32_t idx = ((i * G::FN + j) * 4 + g) * G::NT + tid;
-                f32x4_t v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-                *(f32x4_t*)(ws_tile + (size_t)idx * 4) = v;
+#pragma unroll
+                for (int e = 0; e < 4; e++) st_agent(ws_tile + (size_t)idx * 4 + e, acc[i][j][4 * g + e]);
             }
-    __threadfence();
-    __syncthreads();
     __shared__ uint32_t s_last;
-    if (tid == 0) {
-        uint32_t prev = atomicAdd(&p.semaphores[tile_id], 1u);
-        s_last = (prev == sk - 1) ? 1u : 0u;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
+    if (!publish_and_count(&p.semaphores[tile_id], sk, &s_last)) return;
 #pragma unroll 1
     for (uint32_t i = 0; i < (uint32_t)G::FM; i++) {
 #pragma unroll 1
@@ -357,19 +359,15 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
             const uint32_t idx = (i * G::FN * 4 + jg) * G::NT + tid;
             f32x4_t v = {0.f, 0.f, 0.f, 0.f};
             for (uint32_t q = 0; q < sk; q++) {
-                const float* wq = p.workspace + ((size_t)q * tiles + tile_id) * (BM * BN);
-                f32x4_t w = __builtin_nontemporal_load((const f32x4_t*)(wq + (size_t)idx * 4));
-                v[0] = v[0] + w[0];
-                v[1] = v[1] + w[1];
-                v[2] = v[2] + w[2];
-                v[3] = v[3] + w[3];
+                const float* wq = p.workspace + ((size_t)q * tiles + tile_id) * (BM * BN) + (size_t)idx * 4;
+#pragma unroll
+                for (int e = 0; e < 4; e++) v[e] = v[e] + ld_agent(wq + e);
             }
             *(LDS_AS f32x4_t*)(wreg + l32 * G::EPI_LD + j * 32 + 8 * g + 4 * hi) = v;
         }
         emit_rowblock<G>(p, Cb, wreg, row_base + i * 32, col_base, lane);
     }
-    __syncthreads();
-    if (tid == 0) atomicExch(&p.semaphores[tile_id], 0u);
+    reset_counter(&p.semaphores[tile_id]);
 }
 
 }  // namespace t0
@@ -387,24 +385,25 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
     T0_GEMM_INSTANCE(BM, BN, BK, WM, WN, ST, false, nt) \
     T0_GEMM_INSTANCE(BM, BN, BK, WM, WN, ST, true, nn)
 
-// gfx950-native tiles (auto-selection targets)
+// gfx950-native tiles (auto-selection targets); stages = LDS buffers in flight
 T0_GEMM_BOTH(256, 256, 64, 2, 2, 2)
-T0_GEMM_BOTH(256, 128, 64, 2, 2, 2)
-T0_GEMM_BOTH(128, 256, 64, 2, 2, 2)
-T0_GEMM_BOTH(128, 128, 64, 2, 2, 2)
-T0_GEMM_BOTH(128, 128, 32, 2, 2, 3)
-T0_GEMM_BOTH(128, 64, 64, 2, 2, 2)
-T0_GEMM_BOTH(64, 128, 64, 2, 2, 2)
-T0_GEMM_BOTH(64, 64, 64, 1, 1, 2)
-T0_GEMM_BOTH(32, 64, 64, 1, 1, 2)
-T0_GEMM_BOTH(32, 128, 64, 1, 2, 2)
+T0_GEMM_BOTH(256, 256, 32, 2, 2, 4)
+T0_GEMM_BOTH(256, 128, 64, 2, 2, 3)
+T0_GEMM_BOTH(128, 256, 64, 2, 2, 3)
+T0_GEMM_BOTH(128, 128, 64, 2, 2, 4)
+T0_GEMM_BOTH(128, 128, 32, 2, 2, 4)
+T0_GEMM_BOTH(128, 64, 64, 2, 2, 4)
+T0_GEMM_BOTH(64, 128, 64, 2, 2, 4)
+T0_GEMM_BOTH(64, 64, 64, 1, 1, 4)
+T0_GEMM_BOTH(32, 64, 64, 1, 1, 6)
+T0_GEMM_BOTH(32, 128, 64, 1, 2, 4)
 // the reference's preset geometries (src/t0/gemm_gen.rs:86-145), wave64
-T0_GEMM_BOTH(32, 64, 16, 1, 1, 2)
-T0_GEMM_BOTH(32, 64, 32, 1, 1, 2)
-T0_GEMM_BOTH(32, 128, 16, 1, 1, 2)
-T0_GEMM_BOTH(64, 64, 16, 1, 1, 2)
-T0_GEMM_BOTH(64, 64, 32, 1, 1, 2)
-T0_GEMM_BOTH(128, 64, 16, 2, 1, 2)
-T0_GEMM_BOTH(128, 64, 32, 2, 1, 2)
-T0_GEMM_BOTH(64, 128, 16, 1, 1, 2)
-T0_GEMM_BOTH(128, 128, 16, 2, 1, 2)
+T0_GEMM_BOTH(32, 64, 16, 1, 1, 4)
+T0_GEMM_BOTH(32, 64, 32, 1, 1, 4)
+T0_GEMM_BOTH(32, 128, 16, 1, 1, 4)
+T0_GEMM_BOTH(64, 64, 16, 1, 1, 4)
+T0_GEMM_BOTH(64, 64, 32, 1, 1, 4)
+T0_GEMM_BOTH(128, 64, 16, 2, 1, 4)
+T0_GEMM_BOTH(128, 64, 32, 2, 1, 4)
+T0_GEMM_BOTH(64, 128, 16, 1, 1, 4)
+T0_GEMM_BOTH(128, 128, 16, 2, 1, 4)

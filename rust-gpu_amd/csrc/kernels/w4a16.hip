@@ -74,9 +74,16 @@ template <int WAVES, int MB>
 __device__ __forceinline__ void w4_decode(const t0_w4a16_params& p) {
     constexpr int NCW = 16 * WAVES;
     constexpr int ROWS = 16 * MB;
-    constexpr int KC_MAX = 1024;
+    constexpr int NT = WAVES * 64;
+    constexpr int KC_MAX = 1024 / MB;          // K slice per workgroup (host keeps K/split_k <= this)
+    constexpr int SP_MAX = KC_MAX / 128;       // quant groups (spans) per slice
     constexpr int LDA_S = KC_MAX + 8;          // LDS row stride (elements), +16 B staggers banks
+    constexpr int ACH = ROWS * KC_MAX / 8 / NT;                  // 16-B activation chunks per thread
+    constexpr int SCH = (SP_MAX * NCW + NT - 1) / NT;            // scale / zero entries per thread
+    static_assert(ACH >= 1 && ACH * NT * 8 == ROWS * KC_MAX, "activation staging split");
     __shared__ __attribute__((aligned(16))) uint16_t a_s[ROWS * LDA_S];
+    __shared__ __attribute__((aligned(16))) float s_s[SP_MAX * NCW];
+    __shared__ uint32_t z_s[SP_MAX * NCW];
     __shared__ uint32_t s_last;
 
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -86,25 +93,63 @@ __device__ __forceinline__ void w4_decode(const t0_w4a16_params& p) {
     const uint32_t nb = blockIdx.x, part = blockIdx.y;
     const uint32_t k0 = part * KC;
     const uint32_t spans = KC / 128;
+    const uint32_t g0 = k0 / 128;
     const uint32_t l16 = lane & 15, g4 = lane >> 4;
 
-    // ---- weight stream: one 16-B load per lane per 128-k span ---------------
-    const uint32_t n_src = nb * NCW + wave * 16 + l16;          // column this lane loads
-    const uint32_t* wrow = p.qweight + (size_t)n_src * (K / 8) + (k0 + g4 * 32) / 8;
-    __amdgpu_buffer_rsrc_t rw = make_rsrc(wrow);
-    constexpr int PF = 8;                                        // spans in flight
-    u32x4_t wbuf[PF];
+    // Every load below is unconditional (lanes with nothing to fetch get an
+    // out-of-range offset, which reads zero), issued in this order: the
+    // activation slice, scales and zero points first, then the whole weight
+    // slice.  The LDS staging then waits only for the first group while the
+    // weight bytes stay in flight.
+    // ---- 1. activation slice (rows >= M read as zero) ------------------------
+    const uint32_t chunks_row = KC / 8;
+    __amdgpu_buffer_rsrc_t ra = make_rsrc((const uint16_t*)p.A + k0);
+    u32x4_t areg[ACH];
 #pragma unroll
-    for (int s = 0; s < PF; s++)
-        wbuf[s] = (uint32_t)s < spans ? buffer_load_x4(rw, s * 64) : u32x4_t{0, 0, 0, 0};
+    for (int i = 0; i < ACH; i++) {
+        const uint32_t c = tid + i * NT;
+        const uint32_t r = c / chunks_row, kc = (c % chunks_row) * 8;
+        const bool ok = r < M && c < ROWS * chunks_row;
+        areg[i] = buffer_load_x4(ra, ok ? (r * p.lda + kc) * 2 : OOB_OFFSET);
+    }
+    // ---- 2. scales and zero points of the block's spans ---------------------
+    __amdgpu_buffer_rsrc_t rs = make_rsrc(p.scales);
+    __amdgpu_buffer_rsrc_t rz = make_rsrc(p.zeros ? (const void*)p.zeros : (const void*)p.scales);
+    const bool sf32 = p.flags & T0_W4_SCALE_F32;
+    uint32_t sraw[SCH], zraw[SCH];
+#pragma unroll
+    for (int i = 0; i < SCH; i++) {
+        const uint32_t e = tid + i * NT;
+        const uint32_t sp = e / NCW, n = nb * NCW + e % NCW;
+        const bool ok = e < spans * NCW;
+        const uint32_t gi = (g0 + sp) * N + n;
+        sraw[i] = sf32 ? buffer_load_x1(rs, ok ? gi * 4 : OOB_OFFSET)
+                       : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, ok ? gi * 2 : OOB_OFFSET, 0, 0);
+        zraw[i] = p.zeros ? buffer_load_x1(rz, ok ? ((g0 + sp) * (N / 8) + n / 8) * 4 : OOB_OFFSET) : 0u;
+    }
+    // ---- 3. weight slice: one 16-B load per lane per 128-k span --------------
+    const uint32_t n_src = nb * NCW + wave * 16 + l16;          // column this lane streams
+    __amdgpu_buffer_rsrc_t rw = make_rsrc(p.qweight + (size_t)n_src * (K / 8) + (k0 + g4 * 32) / 8);
+    u32x4_t wbuf[SP_MAX];
+#pragma unroll
+    for (int s = 0; s < SP_MAX; s++) wbuf[s] = buffer_load_x4(rw, (uint32_t)s < spans ? s * 64 : OOB_OFFSET);
 
-    // ---- activation slice -> LDS (rows >= M are zero) -------------------------
-    const uint32_t chunks = ROWS * (KC / 8);
-    for (uint32_t c = tid; c < chunks; c += WAVES * 64) {
-        const uint32_t r = c / (KC / 8), kc = (c % (KC / 8)) * 8;
-        u32x4_t v = {0, 0, 0, 0};
-        if (r < M) v = *(const u32x4_t*)((const uint16_t*)p.A + (size_t)r * p.lda + k0 + kc);
-        *(u32x4_t*)(a_s + r * LDA_S + kc) = v;
+    // ---- 4. stage activations / scales / zero adders into LDS ---------------
+#pragma unroll
+    for (int i = 0; i < ACH; i++) {
+        const uint32_t c = tid + i * NT;
+        const uint32_t r = c / chunks_row, kc = (c % chunks_row) * 8;
+        if (c < ROWS * chunks_row) *(LDS_AS u32x4_t*)((LDS_AS uint16_t*)a_s + r * LDA_S + kc) = areg[i];
+    }
+#pragma unroll
+    for (int i = 0; i < SCH; i++) {
+        const uint32_t e = tid + i * NT;
+        if (e < SP_MAX * NCW) {
+            const uint32_t n = nb * NCW + e % NCW;
+            s_s[e] = sf32 ? __uint_as_float(sraw[i]) : bf16_bits_to_f32(sraw[i] & 0xFFFFu);
+            const uint32_t z = p.zeros ? (zraw[i] >> (4 * (n % 8))) & 0xFu : p.zero_const;
+            z_s[e] = kadd_of(z);
+        }
     }
     __syncthreads();
 
@@ -115,32 +160,25 @@ __device__ __forceinline__ void w4_decode(const t0_w4a16_params& p) {
     for (int mb = 0; mb < MB; mb++) acc[mb] = f32x4_t{0, 0, 0, 0};
     const uint32_t n_out = nb * NCW + wave * 16 + g4 * 4;        // first of this lane's 4 outputs
 
-    for (uint32_t s0 = 0; s0 < spans; s0 += PF) {
 #pragma unroll
-        for (int u = 0; u < PF; u++) {
-            const uint32_t s = s0 + u;
-            if (s >= spans) break;
-            const u32x4_t wq = wbuf[u];
-            if (s + PF < spans) wbuf[u] = buffer_load_x4(rw, (s + PF) * 64);
-            const uint32_t g = (k0 + s * 128) / 128;
-            const uint32_t kadd = kadd_of(zero_of(p, g, n_src));
-            float sc[4];
+    for (int s = 0; s < SP_MAX; s++) {
+        if ((uint32_t)s >= spans) break;
+        const u32x4_t wq = wbuf[s];
+        const uint32_t kadd = z_s[s * NCW + wave * 16 + l16];
+        const f32x4_t sc = *(const LDS_AS f32x4_t*)((const LDS_AS float*)s_s + s * NCW + wave * 16 + g4 * 4);
 #pragma unroll
-            for (int r = 0; r < 4; r++) sc[r] = scale_of(p, g, n_out + r);
+        for (int mb = 0; mb < MB; mb++) {
+            f32x4_t t = {0, 0, 0, 0}, sa = {0, 0, 0, 0};
 #pragma unroll
-            for (int mb = 0; mb < MB; mb++) {
-                f32x4_t t = {0, 0, 0, 0}, sa = {0, 0, 0, 0};
-#pragma unroll
-                for (int w = 0; w < 4; w++) {
-                    const bf16x8_t wv = unpack8(wq[w], kadd);
-                    const bf16x8_t av = *(const LDS_AS bf16x8_t*)(
-                        (const LDS_AS uint16_t*)a_s + (mb * 16 + l16) * LDA_S + s * 128 + g4 * 32 + w * 8);
-                    t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, av, t, 0, 0, 0);
-                    sa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, av, sa, 0, 0, 0);
-                }
-#pragma unroll
-                for (int r = 0; r < 4; r++) acc[mb][r] = fmaf(sc[r], t[r] - 144.0f * sa[r], acc[mb][r]);
+            for (int w = 0; w < 4; w++) {
+                const bf16x8_t wv = unpack8(wq[w], kadd);
+                const bf16x8_t av = *(const LDS_AS bf16x8_t*)(
+                    (const LDS_AS uint16_t*)a_s + (mb * 16 + l16) * LDA_S + s * 128 + g4 * 32 + w * 8);
+                t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, av, t, 0, 0, 0);
+                sa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, av, sa, 0, 0, 0);
             }
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[mb][r] = fmaf(sc[r], t[r] - 144.0f * sa[r], acc[mb][r]);
         }
     }
 
@@ -153,29 +191,25 @@ __device__ __forceinline__ void w4_decode(const t0_w4a16_params& p) {
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) {
         const uint32_t m = mb * 16 + l16;
-        if (m < M) *(f32x4_t*)(p.workspace + ((size_t)part * M + m) * N + n_out) = acc[mb];
+        if (m < M) {
+            float* dst = p.workspace + ((size_t)part * M + m) * N + n_out;
+#pragma unroll
+            for (int e = 0; e < 4; e++) st_agent(dst + e, acc[mb][e]);
+        }
     }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) s_last = (atomicAdd(&p.semaphores[nb], 1u) == sk - 1) ? 1u : 0u;
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
+    if (!publish_and_count(&p.semaphores[nb], sk, &s_last)) return;
     for (uint32_t e = tid; e < (uint32_t)ROWS * (NCW / 4); e += WAVES * 64) {
         const uint32_t m = e / (NCW / 4), n = nb * NCW + (e % (NCW / 4)) * 4;
         if (m >= M) continue;
         f32x4_t v = {0, 0, 0, 0};
         for (uint32_t q = 0; q < sk; q++) {
-            f32x4_t w = __builtin_nontemporal_load((const f32x4_t*)(p.workspace + ((size_t)q * M + m) * N + n));
-            v[0] = v[0] + w[0];
-            v[1] = v[1] + w[1];
-            v[2] = v[2] + w[2];
-            v[3] = v[3] + w[3];
+            const float* src = p.workspace + ((size_t)q * M + m) * N + n;
+#pragma unroll
+            for (int c = 0; c < 4; c++) v[c] = v[c] + ld_agent(src + c);
         }
         store_out4(p, m, n, v);
     }
-    __syncthreads();
-    if (tid == 0) atomicExch(&p.semaphores[nb], 0u);
+    reset_counter(&p.semaphores[nb]);
 }
 
 // ---------------------------------------------------------------------------

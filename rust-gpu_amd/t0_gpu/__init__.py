@@ -31,7 +31,7 @@ PRESETS = ["tile_16x64_k16", "tile_32x64_direct", "tile_32x64_k16", "tile_32x64_
            "tile_64x64_k16", "tile_64x64_k32", "tile_128x64_k16", "tile_64x128_k16", "tile_128x64_k32",
            "tile_128x128_k16", "tile_64x64_k64", "tile_128x128_2pass", "tile_64x128_2pass",
            "tile_256x256_k64", "tile_256x128_k64", "tile_128x256_k64", "tile_128x128_k64", "tile_128x128_k32",
-           "tile_128x64_k64", "tile_64x128_k64", "tile_32x64_k64", "tile_32x128_k64"]
+           "tile_128x64_k64", "tile_64x128_k64", "tile_32x64_k64", "tile_32x128_k64", "tile_256x256_k32"]
 
 
 class T0Error(RuntimeError):
@@ -422,8 +422,41 @@ class GpuRuntime:
     def f32_to_bf16(self, src, dst, count):
         _check(lib().t0_f32_to_bf16(self.h, src, dst, count))
 
+    def capture(self, fn) -> "Graph":
+        """Record everything fn() launches on this runtime's stream into a graph."""
+        _check(lib().t0_graph_begin(self.h))
+        try:
+            fn()
+        except Exception:
+            g = C.c_void_p()
+            lib().t0_graph_end(self.h, C.byref(g))
+            if g:
+                lib().t0_graph_destroy(g)
+            raise
+        g = C.c_void_p()
+        _check(lib().t0_graph_end(self.h, C.byref(g)))
+        return Graph(self, g)
+
+    def copy_device(self, src, dst, nbytes):
+        _check(lib().t0_copy_device(self.h, src, dst, nbytes))
+
     def unpad_2d(self, padded, out, m, n, n_pad):
         _check(lib().t0_unpad_2d(self.h, padded, out, m, n, n_pad))
+
+
+class Graph:
+    def __init__(self, rt: GpuRuntime, handle):
+        self.rt, self.h = rt, handle
+
+    def launch(self):
+        _check(lib().t0_graph_launch(self.rt.h, self.h))
+
+    def __del__(self):
+        try:
+            if self.h:
+                lib().t0_graph_destroy(self.h)
+        except Exception:
+            pass
 
 
 class Event:

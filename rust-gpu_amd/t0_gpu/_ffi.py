@@ -135,6 +135,11 @@ SIGNATURES = {
     "t0_splitk_reduce": ([vp, u64, u64, u32, u64, u32, u32, C.c_int], C.c_int),
     "t0_f32_to_bf16": ([vp, u64, u64, u64], C.c_int),
     "t0_unpad_2d": ([vp, u64, u64, u32, u32, u32], C.c_int),
+    "t0_copy_device": ([vp, u64, u64, u64], C.c_int),
+    "t0_graph_begin": ([vp], C.c_int),
+    "t0_graph_end": ([vp, P(vp)], C.c_int),
+    "t0_graph_launch": ([vp, vp], C.c_int),
+    "t0_graph_destroy": ([vp], C.c_int),
 }
 
 _lib = None
