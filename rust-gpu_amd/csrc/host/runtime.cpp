@@ -1053,6 +1053,8 @@ static int w4_plan(t0_runtime* rt, const t0_w4a16_desc* d, W4Plan& pl) {
         pl.threads = waves * 64;
         pl.split = sk;
         pl.kind = 1;
+        pl.bm = 16 * mb;
+        pl.bn = ncw;
         return T0_OK;
     }
     if (fast && M > 64 && N % 8 == 0 && !d->scales_f32) {
@@ -1109,7 +1111,7 @@ int t0_w4a16_gemm(t0_runtime* rt, const t0_w4a16_desc* d) {
     if (!d->zeros && d->zero_const > 15) return fail(T0_ERR_INVALID, "zero_const must be 0..15");
     hipFunction_t f;
     if (pl.kind == 1 && pl.split > 1) {
-        r = ensure_ws(rt, (size_t)pl.split * p.M * p.N * 4);
+        r = ensure_ws(rt, (size_t)pl.split * pl.gx * pl.bm * pl.bn * 4);   // [column block][split][tile]
         if (r) return r;
         r = ensure_sem(rt, pl.gx);
         if (r) return r;

@@ -84,12 +84,36 @@ T0_DEV bool epi_has_bias(uint32_t ops) {
 // each with its own L2) through agent-scope relaxed atomic stores/loads:
 // these bypass the non-coherent L2, so no cache-wide writeback/invalidate
 // (what a device-scope fence costs) is needed.  Protocol: each workgroup
-// stores its partials with st_agent, waits for its stores (publish()), then
-// bumps a counter; the workgroup that sees the last count reads every
-// partial with ld_agent.
-T0_DEV void st_agent(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-T0_DEV float ld_agent(const float* p) {
-    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// stores its partials with st_agent_x4, waits for its stores
+// (publish_and_count), then bumps a counter; the workgroup that sees the last
+// count reads every partial with ld_agent_x4.
+//
+// Partials move 16 bytes per lane with the sc1 cache-policy bit (the code
+// gfx950 uses for agent-scope relaxed atomics), and a wave covers whole
+// 128-byte lines: write-through stores narrower than a line reach HBM as
+// masked writes, which the memory controller turns into read-modify-writes
+// (a 4-byte-per-lane version of this protocol ran ~20x slower).
+constexpr int CPOL_SC1 = 16;   // aux operand of the raw buffer builtins: sc1
+T0_DEV void st_agent_x4(__amdgpu_buffer_rsrc_t r, uint32_t off, f32x4_t v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, off, 0, CPOL_SC1);
+}
+T0_DEV f32x4_t ld_agent_x4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CPOL_SC1));
+}
+// v += sum over q < n of the 16-byte partials at byte offset off + q*stride, in
+// q order; loads go out eight at a time before any is consumed.
+T0_DEV f32x4_t sum_partials_x4(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t stride, uint32_t n) {
+    f32x4_t v = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+    for (uint32_t q0 = 0; q0 < n; q0 += 8) {
+        f32x4_t t[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) t[j] = ld_agent_x4(r, q0 + j < n ? off + (q0 + j) * stride : OOB_OFFSET);
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (q0 + j < n) v += t[j];
+    }
+    return v;
 }
 // all of this workgroup's stores are performed, then the counter is bumped by
 // one lane; returns true in every thread of the workgroup that arrived last.

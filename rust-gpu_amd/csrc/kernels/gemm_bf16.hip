@@ -338,16 +338,18 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
     // Split-K fixup: every partition parks its partial tile in the workspace
     // (register order, coalesced); the last partition to arrive sums the
     // planes in plane order and runs the epilogue once.
-    float* ws_tile = p.workspace + ((size_t)part * tiles + tile_id) * (BM * BN);
+    // Workspace layout [tile][split][BM*BN f32], register order within a tile.
+    constexpr uint32_t TILE_BYTES = BM * BN * 4;
+    __amdgpu_buffer_rsrc_t rws = make_rsrc((const uint8_t*)p.workspace + (size_t)tile_id * sk * TILE_BYTES);
 #pragma unroll
     for (int i = 0; i < G::FM; i++)
 #pragma unroll
         for (int j = 0; j < G::FN; j++)
 #pragma unroll
             for (int g = 0; g < 4; g++) {
-                uint32_t idx = ((i * G::FN + j) * 4 + g) * G::NT + tid;
-#pragma unroll
-                for (int e = 0; e < 4; e++) st_agent(ws_tile + (size_t)idx * 4 + e, acc[i][j][4 * g + e]);
+                const uint32_t idx = ((i * G::FN + j) * 4 + g) * G::NT + tid;
+                st_agent_x4(rws, part * TILE_BYTES + idx * 16,
+                            f32x4_t{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]});
             }
     __shared__ uint32_t s_last;
     if (!publish_and_count(&p.semaphores[tile_id], sk, &s_last)) return;
@@ -357,12 +359,7 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
         for (uint32_t jg = 0; jg < (uint32_t)G::FN * 4; jg++) {
             const uint32_t j = jg / 4, g = jg % 4;
             const uint32_t idx = (i * G::FN * 4 + jg) * G::NT + tid;
-            f32x4_t v = {0.f, 0.f, 0.f, 0.f};
-            for (uint32_t q = 0; q < sk; q++) {
-                const float* wq = p.workspace + ((size_t)q * tiles + tile_id) * (BM * BN) + (size_t)idx * 4;
-#pragma unroll
-                for (int e = 0; e < 4; e++) v[e] = v[e] + ld_agent(wq + e);
-            }
+            const f32x4_t v = sum_partials_x4(rws, idx * 16, TILE_BYTES, sk);
             *(LDS_AS f32x4_t*)(wreg + l32 * G::EPI_LD + j * 32 + 8 * g + 4 * hi) = v;
         }
         emit_rowblock<G>(p, Cb, wreg, row_base + i * 32, col_base, lane);

@@ -66,8 +66,8 @@ T0_DEV void store_out4(const t0_w4a16_params& p, uint32_t m, uint32_t n, f32x4_t
 //   (lane group l/16 picks which 32 of each 128).  The activation slice sits
 //   in LDS; v_mfma_f32_16x16x32_bf16 with W as the first operand gives lane l
 //   the outputs (m = l%16, n = n0 + 4*(l/16) + r).
-//   split_k > 1: partial sums go to the workspace [split][M][N] and the last
-//   workgroup of each column block adds them in split order.
+//   split_k > 1: partial tiles go to the workspace [column block][split][tile]
+//   and the last workgroup of each column block adds them in split order.
 // Requires: group_size == 128, K % (128*split_k) == 0, N % 16 == 0, lda % 8 == 0.
 // ---------------------------------------------------------------------------
 template <int WAVES, int MB>
@@ -128,11 +128,15 @@ __device__ __forceinline__ void w4_decode(const t0_w4a16_params& p) {
         zraw[i] = p.zeros ? buffer_load_x1(rz, ok ? ((g0 + sp) * (N / 8) + n / 8) * 4 : OOB_OFFSET) : 0u;
     }
     // ---- 3. weight slice: one 16-B load per lane per 128-k span --------------
-    const uint32_t n_src = nb * NCW + wave * 16 + l16;          // column this lane streams
-    __amdgpu_buffer_rsrc_t rw = make_rsrc(p.qweight + (size_t)n_src * (K / 8) + (k0 + g4 * 32) / 8);
+    // The resource base is the wave's first column (wave-uniform: a per-lane
+    // base would make the compiler serialise each load over the distinct
+    // bases); lane l streams column +l%16 at byte offset (l%16)*K/2.
+    const uint32_t n_wave = __builtin_amdgcn_readfirstlane(nb * NCW + wave * 16);
+    __amdgpu_buffer_rsrc_t rw = make_rsrc(p.qweight + (size_t)n_wave * (K / 8) + k0 / 8);
+    const uint32_t w_off = l16 * (K / 2) + g4 * 16;
     u32x4_t wbuf[SP_MAX];
 #pragma unroll
-    for (int s = 0; s < SP_MAX; s++) wbuf[s] = buffer_load_x4(rw, (uint32_t)s < spans ? s * 64 : OOB_OFFSET);
+    for (int s = 0; s < SP_MAX; s++) wbuf[s] = buffer_load_x4(rw, (uint32_t)s < spans ? w_off + s * 64 : OOB_OFFSET);
 
     // ---- 4. stage activations / scales / zero adders into LDS ---------------
 #pragma unroll
@@ -187,28 +191,18 @@ __device__ __forceinline__ void w4_decode(const t0_w4a16_params& p) {
         for (int mb = 0; mb < MB; mb++) store_out4(p, mb * 16 + l16, n_out, acc[mb]);
         return;
     }
-    // split-K: park the partial, last workgroup of the column block reduces
+    // split-K: park the partial tile in the workspace in register order
+    // (tile (part, nb) is ROWS*NCW floats; thread t's 16 bytes of row block mb
+    // at (mb*NT + t)*16), so each wave stores whole lines; the last workgroup
+    // of the column block sums the partitions in partition order.
+    constexpr uint32_t TILE_BYTES = ROWS * NCW * 4;
+    __amdgpu_buffer_rsrc_t rws = make_rsrc((const uint8_t*)p.workspace + (size_t)nb * sk * TILE_BYTES);
 #pragma unroll
-    for (int mb = 0; mb < MB; mb++) {
-        const uint32_t m = mb * 16 + l16;
-        if (m < M) {
-            float* dst = p.workspace + ((size_t)part * M + m) * N + n_out;
-#pragma unroll
-            for (int e = 0; e < 4; e++) st_agent(dst + e, acc[mb][e]);
-        }
-    }
+    for (int mb = 0; mb < MB; mb++) st_agent_x4(rws, part * TILE_BYTES + (mb * NT + tid) * 16, acc[mb]);
     if (!publish_and_count(&p.semaphores[nb], sk, &s_last)) return;
-    for (uint32_t e = tid; e < (uint32_t)ROWS * (NCW / 4); e += WAVES * 64) {
-        const uint32_t m = e / (NCW / 4), n = nb * NCW + (e % (NCW / 4)) * 4;
-        if (m >= M) continue;
-        f32x4_t v = {0, 0, 0, 0};
-        for (uint32_t q = 0; q < sk; q++) {
-            const float* src = p.workspace + ((size_t)q * M + m) * N + n;
 #pragma unroll
-            for (int c = 0; c < 4; c++) v[c] = v[c] + ld_agent(src + c);
-        }
-        store_out4(p, m, n, v);
-    }
+    for (int mb = 0; mb < MB; mb++)
+        store_out4(p, mb * 16 + l16, n_out, sum_partials_x4(rws, (mb * NT + tid) * 16, TILE_BYTES, sk));
     reset_counter(&p.semaphores[nb]);
 }
 
