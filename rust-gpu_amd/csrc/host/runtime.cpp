@@ -1020,7 +1020,6 @@ struct W4Plan {
 };
 
 static int w4_plan(t0_runtime* rt, const t0_w4a16_desc* d, W4Plan& pl) {
-    (void)rt;
     const uint32_t M = d->m, N = d->n, K = d->k, gs = d->group_size;
     if (!M || !N || !K || !gs) return fail(T0_ERR_INVALID, "empty W4A16 problem");
     if (K % 8 || gs % 8 || K % gs) return fail(T0_ERR_INVALID, "K %% 8, gs %% 8 and K %% gs must be 0");
@@ -1030,31 +1029,37 @@ static int w4_plan(t0_runtime* rt, const t0_w4a16_desc* d, W4Plan& pl) {
                           (d->scales % 8) == 0;
     const bool fast = gs == 128 && K % 128 == 0 && align_ok;
     pl = W4Plan();
-    if (fast && M <= 64 && N % 64 == 0) {
+    if (fast && M <= 64 && N % 8 == 0 && d->scales % 16 == 0 && d->zeros % 4 == 0) {
         const uint32_t mb = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
-        const uint32_t waves = (mb == 1 && N % 128 == 0) ? 8 : 4;
-        const uint32_t ncw = 16 * waves;
-        const uint32_t kc_max = 1024 / mb;   // the kernel's K slice limit (LDS staging)
+        const uint32_t kg = 4 / mb;                  // quant groups per pipeline stage
+        const uint32_t cus = rt && rt->cu_count > 0 ? (uint32_t)rt->cu_count : 256;
+        const uint32_t units = N / 4, G = K / 128;
+        // one workgroup per CU, each streaming an even share of the 4-column
+        // units (at least a 16-column tile's worth) over the whole K ...
+        uint32_t wgs = std::min<uint32_t>(cus, (N + 15) / 16);
+        uint32_t tiles = (4 * ((units + wgs - 1) / wgs) + 15) / 16;
+        if (tiles > 4) {                             // ... or 64-column ranges
+            wgs = (units + 15) / 16;
+            tiles = 4;
+        }
         uint32_t sk = d->split_k;
         if (!sk) {
-            // enough workgroups to cover the CUs a few times within the slice limit
+            // narrow N: split K over otherwise idle CUs, a stage or more each
             sk = 1;
-            while (sk < 16 && ((uint64_t)(N / ncw) * sk < 512 || K / sk > kc_max) && (K / (2 * sk)) % 128 == 0 &&
-                   K / (2 * sk) >= 128)
-                sk *= 2;
+            while ((uint64_t)wgs * sk * 2 <= cus && G % (2 * sk) == 0 && G / (2 * sk) >= kg) sk *= 2;
         }
-        if (K % (128 * sk) || K / sk > kc_max)
-            return fail(T0_ERR_INVALID, "split_k %u does not fit K %u (slice <= %u)", sk, K, kc_max);
+        if (G % sk)
+            return fail(T0_ERR_INVALID, "split_k %u must divide the %u quant groups of K", sk, G);
         char b[64];
-        snprintf(b, sizeof b, "t0k_w4a16_decode_w%u_mb%u", waves, mb);
+        snprintf(b, sizeof b, "t0k_w4a16_decode_t%u_mb%u", tiles, mb);
         pl.sym = b;
-        pl.gx = N / ncw;
+        pl.gx = wgs;
         pl.gy = sk;
-        pl.threads = waves * 64;
+        pl.threads = 64 * t0_w4_decode_waves((int)tiles, (int)mb);
         pl.split = sk;
         pl.kind = 1;
         pl.bm = 16 * mb;
-        pl.bn = ncw;
+        pl.bn = 16 * tiles;
         return T0_OK;
     }
     if (fast && M > 64 && N % 8 == 0 && !d->scales_f32) {

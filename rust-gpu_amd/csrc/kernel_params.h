@@ -46,19 +46,20 @@ typedef struct t0_gemm_params {
 } t0_gemm_params;
 
 // W4A16: C[M,N] = A[M,K] (bf16) . W^T, W given as GPTQ-packed int4
-// [N][K/8] u32 words (k at bits 4*(k%8)), scales [N][K/gs] (bf16 or f32),
-// zero points either the constant zero_const (zeros == NULL) or packed 4-bit
-// [N][ceil(G/8)] u32 words (group g at bits 4*(g%8)).
+// [N][K/8] u32 words (k at bits 4*(k%8)), scales [G][N] (bf16 or f32,
+// G = K/group_size), zero points either the constant zero_const
+// (zeros == NULL) or packed 4-bit [G][N/8] u32 words (column n at bits
+// 4*(n%8)).
 #define T0_W4_SCALE_F32 0x1u   // scales are f32 (else bf16)
 #define T0_W4_OUT_F32 0x2u     // store f32 (else bf16 RNE)
 
 typedef struct t0_w4a16_params {
     const void* A;            // bf16 [M, lda]
     const uint32_t* qweight;  // [N][K/8]
-    const void* scales;       // [N][G]
-    const uint32_t* zeros;    // [N][ceil(G/8)] or NULL
+    const void* scales;       // [G][N]
+    const uint32_t* zeros;    // [G][N/8] or NULL
     void* C;                  // [M, ldc]
-    float* workspace;         // decode split-K partial planes
+    float* workspace;         // decode split-K partial tiles; prefill group sums
     uint32_t* semaphores;     // decode split-K counters
     uint32_t M, N, K;
     uint32_t lda, ldc;
@@ -92,5 +93,11 @@ typedef struct t0_aux_params {
 } t0_aux_params;
 
 #ifdef __cplusplus
+}
+
+// Waves per workgroup of t0k_w4a16_decode_t<tiles>_mb<mb>: 16 (4 per SIMD,
+// <= 128 VGPRs each) when a wave's per-group registers allow, else 8 or 4.
+constexpr int t0_w4_decode_waves(int tiles, int mb) {
+    return (tiles * mb <= 3 && 32 / mb >= 16) ? 16 : (tiles * mb <= 8 ? 8 : 4);
 }
 #endif

@@ -32,8 +32,34 @@ T0_DEV void load_lds_x4(__amdgpu_buffer_rsrc_t r, LDS_AS void* lds_wave_base, ui
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds_wave_base, 16, voffset, 0, 0, 0);
 }
 
+// s_waitcnt vmcnt(N) alone.  gfx9 encoding: vmcnt[3:0] | expcnt[6:4] |
+// lgkmcnt[11:8] | vmcnt_hi[15:14]; the other counters are left at their max.
+template <int N>
+T0_DEV void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+
+// Global (rsrc + voffset) -> LDS (m0 + lane*16, resp. m0 + lane*4) without
+// VGPR staging.  Issued as inline asm: the compiler cannot see which LDS
+// buffer the DMA targets and would otherwise wait for it (vmcnt(0)) before
+// every LDS read; callers track completion with explicit wait_vmcnt.
+// lds_addr must be wave-uniform.
+T0_DEV void dma_x4(__amdgpu_buffer_rsrc_t r, uint32_t lds_addr, uint32_t voffset) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :: "s"(lds_addr), "v"(voffset), "s"(r) : "memory");
+}
+T0_DEV void dma_x1(__amdgpu_buffer_rsrc_t r, uint32_t lds_addr, uint32_t voffset) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+                 :: "s"(lds_addr), "v"(voffset), "s"(r) : "memory");
+}
+
 T0_DEV u32x4_t buffer_load_x4(__amdgpu_buffer_rsrc_t r, uint32_t voffset) {
     return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, 0, 0));
+}
+
+T0_DEV u32x2_t buffer_load_x2(__amdgpu_buffer_rsrc_t r, uint32_t voffset) {
+    return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(r, voffset, 0, 0));
 }
 
 T0_DEV uint32_t buffer_load_x1(__amdgpu_buffer_rsrc_t r, uint32_t voffset) {

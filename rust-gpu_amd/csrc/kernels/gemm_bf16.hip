@@ -67,22 +67,6 @@ struct GemmCfg {
     static_assert(STAGE_BYTES * STAGES <= 160 * 1024, "LDS");
 };
 
-template <int N>
-T0_DEV void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
-}
-
-// 16 bytes per lane, global (rsrc + voffset) -> LDS (m0 + lane*16).  Issued
-// as inline asm: the compiler cannot see which LDS buffer the DMA targets and
-// would otherwise wait for it (vmcnt(0)) before every LDS read; the K loop
-// tracks completion itself with explicit vmcnt waits.
-T0_DEV void dma_x4(__amdgpu_buffer_rsrc_t r, uint32_t lds_addr, uint32_t voffset) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                 :: "s"(lds_addr), "v"(voffset), "s"(r) : "memory");
-}
-
 template <class G>
 struct TileLoader {
     // per-lane byte offsets relative to the stage's tile base, or OOB

@@ -59,151 +59,291 @@ T0_DEV void store_out4(const t0_w4a16_params& p, uint32_t m, uint32_t n, f32x4_t
 }
 
 // ---------------------------------------------------------------------------
-// Decode: small M (<= 16*MB), memory bound.
-//   grid = (N / (16*WAVES), split_k), block = 64*WAVES.
-//   Workgroup: 16*WAVES columns x K-slice of K/split_k (multiple of 128).
-//   Wave: 16 columns; lane l streams column n0 + l%16, 32 k per 16-byte load
-//   (lane group l/16 picks which 32 of each 128).  The activation slice sits
-//   in LDS; v_mfma_f32_16x16x32_bf16 with W as the first operand gives lane l
-//   the outputs (m = l%16, n = n0 + 4*(l/16) + r).
-//   split_k > 1: partial tiles go to the workspace [column block][split][tile]
-//   and the last workgroup of each column block adds them in split order.
-// Requires: group_size == 128, K % (128*split_k) == 0, N % 16 == 0, lda % 8 == 0.
+// Decode: small M (<= 16*MB), HBM bound.
+//   grid = (WG, split_k), block = 64*WAVES; the host sizes WG to the CU count,
+//   so each workgroup (alone on its CU) streams one contiguous column range
+//   over its whole K slice and, with split_k == 1, no partial sums leave the
+//   CU.  Workgroup i owns columns [c0, c1): the 4-column units of N split
+//   evenly over gridDim.x, at most 16*TILES columns.
+//   The slice is walked in passes of KP = 32/MB quant groups (128 k each).
+//   A pass first issues every load it needs, so the whole pass is in flight
+//   at once (HBM latency is the enemy at this size):
+//     A  [16*MB rows][KP*256 B]  -> LDS by buffer_load ... lds (rows >= M are
+//                                   skipped), 16-B chunks XOR-swizzled by row
+//     S  [KP][16 x 16 B]         -> LDS, scales from column c0 (bf16: c0
+//                                   rounded down to 8)
+//     Z  [KP][16 words]          -> LDS, packed zero points from word c0/8
+//     W  -> VGPRs: wave w takes groups w, w+WAVES, ... of the pass; lane l
+//           (c = l%16, h = l/16) loads, per group and tile t, the 16 bytes of
+//           column c0 + 16t + c holding k = 128g + 32h + [0, 32).
+//   Per group, v_mfma_f32_16x16x32_bf16(W, A) with W = bf16(128 + q) gives
+//   lane l T = sum_k a*(128 + q) for outputs (m = 16mb + c,
+//   n = c0 + 16t + 4h + r), r = 0..3; a ones-MFMA gives sum_k a, and
+//   acc += s * (T - (128 + z) * sum a).  The waves are summed in wave order
+//   through LDS at the end.
+//   split_k > 1 (narrow N): partition blockIdx.y covers G/split_k groups; the
+//   workgroup's tile goes to the workspace [i][split][tile] and the last
+//   partition to arrive adds them in split order.
+// Requires: group_size == 128, K % 128 == 0, (K/128) % split_k == 0,
+//           N % 8 == 0, lda % 8 == 0, 16-byte aligned A / qweight / scales.
 // ---------------------------------------------------------------------------
-template <int WAVES, int MB>
-__device__ __forceinline__ void w4_decode(const t0_w4a16_params& p) {
-    constexpr int NCW = 16 * WAVES;
-    constexpr int ROWS = 16 * MB;
-    constexpr int NT = WAVES * 64;
-    constexpr int KC_MAX = 1024 / MB;          // K slice per workgroup (host keeps K/split_k <= this)
-    constexpr int SP_MAX = KC_MAX / 128;       // quant groups (spans) per slice
-    constexpr int LDA_S = KC_MAX + 8;          // LDS row stride (elements), +16 B staggers banks
-    constexpr int ACH = ROWS * KC_MAX / 8 / NT;                  // 16-B activation chunks per thread
-    constexpr int SCH = (SP_MAX * NCW + NT - 1) / NT;            // scale / zero entries per thread
-    static_assert(ACH >= 1 && ACH * NT * 8 == ROWS * KC_MAX, "activation staging split");
-    __shared__ __attribute__((aligned(16))) uint16_t a_s[ROWS * LDA_S];
-    __shared__ __attribute__((aligned(16))) float s_s[SP_MAX * NCW];
-    __shared__ uint32_t z_s[SP_MAX * NCW];
-    __shared__ uint32_t s_last;
 
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t K = p.K, N = p.N, M = p.M;
-    const uint32_t sk = p.split_k;
-    const uint32_t KC = K / sk;
-    const uint32_t nb = blockIdx.x, part = blockIdx.y;
-    const uint32_t k0 = part * KC;
-    const uint32_t spans = KC / 128;
-    const uint32_t g0 = k0 / 128;
-    const uint32_t l16 = lane & 15, g4 = lane >> 4;
+// 8 nibbles of one u32 (k = 0..7) -> 8 bf16 of value 128 + q, in k order:
+// dword i = bytes (w.byte_i, -, (w >> 4).byte_i, -) masked to the low nibbles
+// and or-ed into 0x4300 (= 128.0).
+// The mask-and-insert is one v_and_or_b32 (the compiler would split it in
+// two: a VOP3 here cannot take the literal, so the constants come in
+// registers, one scalar and one vector).
+T0_DEV uint32_t and_or(uint32_t x, uint32_t mask, uint32_t bits) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(mask), "v"(bits));
+    return r;
+}
+T0_DEV bf16x8_t unpack8_128(uint32_t w, uint32_t bits4300) {
+    const uint32_t t = w >> 4;
+    u32x4_t r;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        r[i] = and_or(__builtin_amdgcn_perm(t, w, 0x0C000C00u | ((4u + i) << 16) | (uint32_t)i), 0x000F000Fu, bits4300);
+    return __builtin_bit_cast(bf16x8_t, r);
+}
 
-    // Every load below is unconditional (lanes with nothing to fetch get an
-    // out-of-range offset, which reads zero), issued in this order: the
-    // activation slice, scales and zero points first, then the whole weight
-    // slice.  The LDS staging then waits only for the first group while the
-    // weight bytes stay in flight.
-    // ---- 1. activation slice (rows >= M read as zero) ------------------------
-    const uint32_t chunks_row = KC / 8;
-    __amdgpu_buffer_rsrc_t ra = make_rsrc((const uint16_t*)p.A + k0);
-    u32x4_t areg[ACH];
-#pragma unroll
-    for (int i = 0; i < ACH; i++) {
-        const uint32_t c = tid + i * NT;
-        const uint32_t r = c / chunks_row, kc = (c % chunks_row) * 8;
-        const bool ok = r < M && c < ROWS * chunks_row;
-        areg[i] = buffer_load_x4(ra, ok ? (r * p.lda + kc) * 2 : OOB_OFFSET);
-    }
-    // ---- 2. scales and zero points of the block's spans ---------------------
-    __amdgpu_buffer_rsrc_t rs = make_rsrc(p.scales);
-    __amdgpu_buffer_rsrc_t rz = make_rsrc(p.zeros ? (const void*)p.zeros : (const void*)p.scales);
-    const bool sf32 = p.flags & T0_W4_SCALE_F32;
-    uint32_t sraw[SCH], zraw[SCH];
-#pragma unroll
-    for (int i = 0; i < SCH; i++) {
-        const uint32_t e = tid + i * NT;
-        const uint32_t sp = e / NCW, n = nb * NCW + e % NCW;
-        const bool ok = e < spans * NCW;
-        const uint32_t gi = (g0 + sp) * N + n;
-        sraw[i] = sf32 ? buffer_load_x1(rs, ok ? gi * 4 : OOB_OFFSET)
-                       : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, ok ? gi * 2 : OOB_OFFSET, 0, 0);
-        zraw[i] = p.zeros ? buffer_load_x1(rz, ok ? ((g0 + sp) * (N / 8) + n / 8) * 4 : OOB_OFFSET) : 0u;
-    }
-    // ---- 3. weight slice: one 16-B load per lane per 128-k span --------------
-    // The resource base is the wave's first column (wave-uniform: a per-lane
-    // base would make the compiler serialise each load over the distinct
-    // bases); lane l streams column +l%16 at byte offset (l%16)*K/2.
-    const uint32_t n_wave = __builtin_amdgcn_readfirstlane(nb * NCW + wave * 16);
-    __amdgpu_buffer_rsrc_t rw = make_rsrc(p.qweight + (size_t)n_wave * (K / 8) + k0 / 8);
-    const uint32_t w_off = l16 * (K / 2) + g4 * 16;
-    u32x4_t wbuf[SP_MAX];
-#pragma unroll
-    for (int s = 0; s < SP_MAX; s++) wbuf[s] = buffer_load_x4(rw, (uint32_t)s < spans ? w_off + s * 64 : OOB_OFFSET);
+template <int TILES, int MB>
+struct W4DecCfg {
+    static constexpr int KP = 32 / MB;                   // quant groups per pass
+    // as many waves as the per-group registers allow (16 waves: <= 128 VGPRs)
+    static constexpr int WAVES = t0_w4_decode_waves(TILES, MB), NT = 64 * WAVES;
+    static constexpr int GPW = KP / WAVES;               // groups per wave per pass
+    static constexpr int RA = KP * 256;                  // A row bytes per pass
+    static constexpr int A_BYTES = 16 * MB * RA;         // 128 KB
+    static constexpr int S_OFF = A_BYTES, S_BYTES = KP * 256;
+    static constexpr int Z_OFF = S_OFF + S_BYTES, Z_BYTES = KP * 64;
+    static constexpr int SMEM = Z_OFF + Z_BYTES;
+    static constexpr int A_DMA = A_BYTES / 1024 / WAVES; // A DMA loads per wave
+    static constexpr int S_BLOCKS = KP * 16 / 64;        // S (16 B/lane) and Z (4 B/lane) DMA blocks
+    static constexpr int S_DMA = (S_BLOCKS + WAVES - 1) / WAVES;   // per wave (block i*WAVES + wave)
+    static constexpr int W_LOADS = GPW * TILES;          // weight loads per lane per pass
+    static constexpr int OUT_SLOTS = TILES * MB * 64;    // 16-byte outputs per workgroup
+    static_assert(GPW * WAVES == KP && A_DMA * WAVES * 1024 == A_BYTES, "pass split");
+    static_assert(S_BLOCKS * 64 == KP * 16, "S/Z split");
+    static_assert(W_LOADS < 64, "vmcnt range");
+    static_assert(WAVES * OUT_SLOTS * 16 <= A_BYTES, "reduction fits the A buffer");
+    static_assert(SMEM <= 160 * 1024, "LDS");
+};
 
-    // ---- 4. stage activations / scales / zero adders into LDS ---------------
-#pragma unroll
-    for (int i = 0; i < ACH; i++) {
-        const uint32_t c = tid + i * NT;
-        const uint32_t r = c / chunks_row, kc = (c % chunks_row) * 8;
-        if (c < ROWS * chunks_row) *(LDS_AS u32x4_t*)((LDS_AS uint16_t*)a_s + r * LDA_S + kc) = areg[i];
-    }
-#pragma unroll
-    for (int i = 0; i < SCH; i++) {
-        const uint32_t e = tid + i * NT;
-        if (e < SP_MAX * NCW) {
-            const uint32_t n = nb * NCW + e % NCW;
-            s_s[e] = sf32 ? __uint_as_float(sraw[i]) : bf16_bits_to_f32(sraw[i] & 0xFFFFu);
-            const uint32_t z = p.zeros ? (zraw[i] >> (4 * (n % 8))) & 0xFu : p.zero_const;
-            z_s[e] = kadd_of(z);
-        }
-    }
-    __syncthreads();
+template <int TILES, int MB, bool ZP, bool SF32>
+__device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, uint8_t* smem, uint32_t* s_last) {
+    using G = W4DecCfg<TILES, MB>;
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t K = p.K, N = p.N, M = p.M, sk = p.split_k;
+    const uint32_t wg = blockIdx.x, part = blockIdx.y;
+    const uint32_t units = N / 4;
+    const uint32_t c0 = 4 * (uint32_t)((uint64_t)wg * units / gridDim.x);
+    const uint32_t c1 = 4 * (uint32_t)((uint64_t)(wg + 1) * units / gridDim.x);
+    const uint32_t GP = K / 128 / sk;                   // groups in this partition
+    const uint32_t g_begin = part * GP, g_end = g_begin + GP;
+    const uint32_t sb = SF32 ? c0 : (c0 & ~7u);          // first column of the S chunks
+    const uint32_t zb = c0 / 8;                          // first word of the Z chunks
+    const uint32_t s_row = N * (SF32 ? 4 : 2), z_row = (N / 8) * 4;
+    const uint32_t c = lane & 15, h = lane >> 4;
 
-    // bf16 1.0 x 8 for the activation-sum MFMA
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.scales);
+    const __amdgpu_buffer_rsrc_t rz = make_rsrc(ZP ? (const void*)p.zeros : p.scales);
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.qweight + (size_t)c0 * (K / 8));
+    const uint32_t lds_base = (uint32_t)(uintptr_t)(LDS_AS uint8_t*)smem;
+
+    // ---- loop-invariant per-lane offsets ------------------------------------
+    // A DMA block b = wave*A_DMA + i covers LDS bytes [b KB, (b+1) KB): row r,
+    // LDS chunk cl, global chunk cl ^ (r & 15) of the pass's k range.
+    uint32_t a_off[G::A_DMA];
+#pragma unroll
+    for (int i = 0; i < G::A_DMA; i++) {
+        const uint32_t pos = (wave * G::A_DMA + i) * 1024 + lane * 16;
+        const uint32_t r = pos / G::RA, cl = (pos % G::RA) / 16;
+        const uint32_t cg = (cl & ~15u) | ((cl ^ r) & 15u);
+        a_off[i] = r * p.lda * 2 + cg * 16;
+    }
+    // S / Z DMA: lane of block b = i*WAVES + wave serves group q = (b*64 + lane)/16
+    // of the pass, chunk (word) lane % 16
+    uint32_t s_off[G::S_DMA], z_off[G::S_DMA];
+#pragma unroll
+    for (int i = 0; i < G::S_DMA; i++) {
+        const uint32_t e = (i * G::WAVES + wave) * 64 + lane, q = e / 16, k16 = e % 16;
+        const uint32_t col = sb + k16 * (SF32 ? 4 : 8);
+        s_off[i] = (col < N && col < c1) ? q * s_row + (SF32 ? col * 4 : col * 2) : OOB_OFFSET;
+        z_off[i] = (ZP && zb + k16 < N / 8 && (zb + k16) * 8 < c1) ? q * z_row + (zb + k16) * 4 : OOB_OFFSET;
+    }
+    // weight rows of this lane (column c0 + 16t + c), OOB past c1
+    uint32_t w_row[TILES];
+#pragma unroll
+    for (int t = 0; t < TILES; t++) w_row[t] = c0 + 16 * t + c < c1 ? (16 * t + c) * (K / 2) + 16 * h : OOB_OFFSET;
+    // per-tile reads of this lane's 4 output columns n4 .. n4+3
+    uint32_t s_rd[TILES], z_rd[TILES], z_sh[TILES];
+#pragma unroll
+    for (int t = 0; t < TILES; t++) {
+        const uint32_t n4 = c0 + 16 * t + 4 * h;
+        s_rd[t] = G::S_OFF + (n4 - sb) * (SF32 ? 4 : 2);
+        z_rd[t] = G::Z_OFF + (n4 / 8 - zb) * 4;
+        z_sh[t] = 4 * (n4 % 8);
+    }
+    const float zc_const = 128.0f + (float)p.zero_const;
+    const uint32_t bits4300 = __builtin_amdgcn_mov_dpp(0x43004300u, 0xE4, 0xF, 0xF, false);  // in a VGPR
     const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, u32x4_t{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
-    f32x4_t acc[MB];
+    f32x4_t acc[TILES][MB];
 #pragma unroll
-    for (int mb = 0; mb < MB; mb++) acc[mb] = f32x4_t{0, 0, 0, 0};
-    const uint32_t n_out = nb * NCW + wave * 16 + g4 * 4;        // first of this lane's 4 outputs
+    for (int t = 0; t < TILES; t++)
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++) acc[t][mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
+#pragma unroll 1
+    for (uint32_t g0 = g_begin; g0 < g_end; g0 += G::KP) {
+        const uint32_t np = min((uint32_t)G::KP, g_end - g0);   // groups in this pass
+        if (g0 != g_begin) __syncthreads();                      // previous pass done with LDS
+        // ---- 1. A, S, Z -> LDS ----------------------------------------------
 #pragma unroll
-    for (int s = 0; s < SP_MAX; s++) {
-        if ((uint32_t)s >= spans) break;
-        const u32x4_t wq = wbuf[s];
-        const uint32_t kadd = z_s[s * NCW + wave * 16 + l16];
-        const f32x4_t sc = *(const LDS_AS f32x4_t*)((const LDS_AS float*)s_s + s * NCW + wave * 16 + g4 * 4);
+        for (int i = 0; i < G::A_DMA; i++) {
+            const uint32_t b = wave * G::A_DMA + i;
+            const uint32_t r = b * 1024 / G::RA;                 // wave-uniform row
+            if (r < M) {
+                const uint32_t cl = ((b * 1024) % G::RA) / 16 + lane;   // chunk of this lane
+                const bool ok = cl / 16 < np;
+                dma_x4(ra, __builtin_amdgcn_readfirstlane(lds_base + b * 1024), ok ? a_off[i] + g0 * 256 : OOB_OFFSET);
+            }
+        }
 #pragma unroll
-        for (int mb = 0; mb < MB; mb++) {
-            f32x4_t t = {0, 0, 0, 0}, sa = {0, 0, 0, 0};
+        for (int i = 0; i < G::S_DMA; i++) {
+            const uint32_t b = i * G::WAVES + wave;
+            if (b >= (uint32_t)G::S_BLOCKS) break;               // wave-uniform
+            const bool ok = (b * 64 + lane) / 16 < np;
+            dma_x4(rs, __builtin_amdgcn_readfirstlane(lds_base + G::S_OFF + b * 1024), ok ? s_off[i] + g0 * s_row : OOB_OFFSET);
+            if (ZP) dma_x1(rz, __builtin_amdgcn_readfirstlane(lds_base + G::Z_OFF + b * 256), ok ? z_off[i] + g0 * z_row : OOB_OFFSET);
+        }
+        // ---- 2. weights -> VGPRs, in the order they are consumed ------------
+        u32x4_t wq[G::GPW][TILES];
 #pragma unroll
-            for (int w = 0; w < 4; w++) {
-                const bf16x8_t wv = unpack8(wq[w], kadd);
-                const bf16x8_t av = *(const LDS_AS bf16x8_t*)(
-                    (const LDS_AS uint16_t*)a_s + (mb * 16 + l16) * LDA_S + s * 128 + g4 * 32 + w * 8);
-                t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, av, t, 0, 0, 0);
-                sa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, av, sa, 0, 0, 0);
+        for (int j = 0; j < G::GPW; j++) {
+            const uint32_t gl = wave + G::WAVES * j;            // group within the pass
+#pragma unroll
+            for (int t = 0; t < TILES; t++)
+                wq[j][t] = buffer_load_x4(rw, gl < np ? w_row[t] + (g0 + gl) * 64 : OOB_OFFSET);
+        }
+        // ---- 3. the DMAs (issued before every weight load) are done ---------
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt<G::W_LOADS>();
+        __syncthreads();
+        // ---- 4. consume the groups as their weights arrive (a group past the
+        // pass read zeros everywhere and adds exactly 0; no early exit, so no
+        // load is left in flight into the next pass's registers) -----------
+        const LDS_AS uint8_t* sp = (const LDS_AS uint8_t*)smem;
+#pragma unroll
+        for (int j = 0; j < G::GPW; j++) {
+            const uint32_t gl = wave + G::WAVES * j;
+            f32x4_t s4[TILES], zc[TILES];
+#pragma unroll
+            for (int t = 0; t < TILES; t++) {
+                const u32x2_t lo = *(const LDS_AS u32x2_t*)(sp + s_rd[t] + gl * 256);
+                if (SF32) {
+                    const u32x2_t hi = *(const LDS_AS u32x2_t*)(sp + s_rd[t] + gl * 256 + 8);
+                    s4[t] = f32x4_t{__uint_as_float(lo[0]), __uint_as_float(lo[1]), __uint_as_float(hi[0]), __uint_as_float(hi[1])};
+                } else {
+                    s4[t] = f32x4_t{bf16_bits_to_f32(lo[0] & 0xFFFFu), bf16_bits_to_f32(lo[0] >> 16),
+                                    bf16_bits_to_f32(lo[1] & 0xFFFFu), bf16_bits_to_f32(lo[1] >> 16)};
+                }
+                if (ZP) {
+                    const uint32_t zw = *(const LDS_AS uint32_t*)(sp + z_rd[t] + gl * 64) >> z_sh[t];
+#pragma unroll
+                    for (int r = 0; r < 4; r++) zc[t][r] = 128.0f + (float)((zw >> (4 * r)) & 0xFu);
+                } else {
+                    zc[t] = f32x4_t{zc_const, zc_const, zc_const, zc_const};
+                }
+            }
+            // activation fragments and sums of every row block, then one tile
+            // at a time: unpack its weights once, use them for every row block
+            bf16x8_t av[MB][4];
+            f32x4_t sa[MB];
+#pragma unroll
+            for (int mb = 0; mb < MB; mb++) {
+                const uint32_t row = 16 * mb + c;
+#pragma unroll
+                for (int w = 0; w < 4; w++)
+                    av[mb][w] = *(const LDS_AS bf16x8_t*)(sp + row * G::RA + gl * 256 + (((4 * h + w) ^ c) * 16));
+                sa[mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int w = 0; w < 4; w++) sa[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, av[mb][w], sa[mb], 0, 0, 0);
             }
 #pragma unroll
-            for (int r = 0; r < 4; r++) acc[mb][r] = fmaf(sc[r], t[r] - 144.0f * sa[r], acc[mb][r]);
+            for (int t = 0; t < TILES; t++) {
+                bf16x8_t wv[4];
+#pragma unroll
+                for (int w = 0; w < 4; w++) wv[w] = unpack8_128(wq[j][t][w], bits4300);
+#pragma unroll
+                for (int mb = 0; mb < MB; mb++) {
+                    f32x4_t tt = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int w = 0; w < 4; w++) tt = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv[w], av[mb][w], tt, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) acc[t][mb][r] = fmaf(s4[t][r], fmaf(-zc[t][r], sa[mb][r], tt[r]), acc[t][mb][r]);
+                }
+            }
         }
     }
 
-    if (sk == 1) {
+    // ---- sum the waves, in wave order ----------------------------------------
+    __syncthreads();                                     // LDS free for the reduction
+    LDS_AS f32x4_t* red = (LDS_AS f32x4_t*)(LDS_AS uint8_t*)smem;
 #pragma unroll
-        for (int mb = 0; mb < MB; mb++) store_out4(p, mb * 16 + l16, n_out, acc[mb]);
-        return;
+    for (int t = 0; t < TILES; t++)
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++) red[(wave * TILES * MB + t * MB + mb) * 64 + lane] = acc[t][mb];
+    __syncthreads();
+    constexpr uint32_t TILE_BYTES = G::OUT_SLOTS * 16;
+    constexpr int NE = (G::OUT_SLOTS + G::NT - 1) / G::NT;
+    const __amdgpu_buffer_rsrc_t rws = make_rsrc((const uint8_t*)p.workspace + (size_t)wg * sk * TILE_BYTES);
+    f32x4_t v[NE];
+#pragma unroll
+    for (int e = 0; e < NE; e++) {
+        const uint32_t slot = e * G::NT + tid;          // (t, mb, lane)
+        v[e] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        if (slot < (uint32_t)G::OUT_SLOTS) {
+#pragma unroll
+            for (int q = 0; q < G::WAVES; q++) v[e] += red[q * G::OUT_SLOTS + slot];
+            if (sk > 1) st_agent_x4(rws, part * TILE_BYTES + slot * 16, v[e]);
+        }
     }
-    // split-K: park the partial tile in the workspace in register order
-    // (tile (part, nb) is ROWS*NCW floats; thread t's 16 bytes of row block mb
-    // at (mb*NT + t)*16), so each wave stores whole lines; the last workgroup
-    // of the column block sums the partitions in partition order.
-    constexpr uint32_t TILE_BYTES = ROWS * NCW * 4;
-    __amdgpu_buffer_rsrc_t rws = make_rsrc((const uint8_t*)p.workspace + (size_t)nb * sk * TILE_BYTES);
+    if (sk > 1) {
+        if (!publish_and_count(&p.semaphores[wg], sk, s_last)) return;
 #pragma unroll
-    for (int mb = 0; mb < MB; mb++) st_agent_x4(rws, part * TILE_BYTES + (mb * NT + tid) * 16, acc[mb]);
-    if (!publish_and_count(&p.semaphores[nb], sk, &s_last)) return;
+        for (int e = 0; e < NE; e++) {
+            const uint32_t slot = e * G::NT + tid;
+            if (slot < (uint32_t)G::OUT_SLOTS) v[e] = sum_partials_x4(rws, slot * 16, TILE_BYTES, sk);
+        }
+    }
 #pragma unroll
-    for (int mb = 0; mb < MB; mb++)
-        store_out4(p, mb * 16 + l16, n_out, sum_partials_x4(rws, (mb * NT + tid) * 16, TILE_BYTES, sk));
-    reset_counter(&p.semaphores[nb]);
+    for (int e = 0; e < NE; e++) {
+        const uint32_t slot = e * G::NT + tid;
+        if (slot >= (uint32_t)G::OUT_SLOTS) continue;
+        const uint32_t t = slot / (MB * 64), mb = (slot / 64) % MB, l = slot % 64;
+        const uint32_t n = c0 + 16 * t + 4 * (l >> 4);
+        if (n < c1) store_out4(p, 16 * mb + (l & 15), n, v[e]);
+    }
+    if (sk > 1) reset_counter(&p.semaphores[wg]);
+}
+
+template <int TILES, int MB>
+__device__ __forceinline__ void w4_decode(const t0_w4a16_params& p) {
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[W4DecCfg<TILES, MB>::SMEM];
+    __shared__ uint32_t s_last;
+    // zero points and scale type are uniform: one straight-line body each
+    const bool zp = p.zeros != nullptr, sf32 = p.flags & T0_W4_SCALE_F32;
+    if (zp) {
+        if (sf32) w4_decode_body<TILES, MB, true, true>(p, smem, &s_last);
+        else w4_decode_body<TILES, MB, true, false>(p, smem, &s_last);
+    } else {
+        if (sf32) w4_decode_body<TILES, MB, false, true>(p, smem, &s_last);
+        else w4_decode_body<TILES, MB, false, false>(p, smem, &s_last);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -242,16 +382,6 @@ struct W4Cfg {
     static_assert(SMEM <= 160 * 1024, "LDS");
     static_assert(NW >= 2 && STAGES == 2, "scale/X DMA split over two waves; vmcnt(0) per stage");
 };
-
-template <int N_>
-T0_DEV void w4_wait_vmcnt() {
-    __builtin_amdgcn_s_waitcnt((N_ & 0xF) | (0x7 << 4) | (0xF << 8) | ((N_ >> 4) << 14));
-}
-
-T0_DEV void w4_dma(__amdgpu_buffer_rsrc_t r, uint32_t lds_addr, uint32_t voffset) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                 :: "s"(lds_addr), "v"(voffset), "s"(r) : "memory");
-}
 
 template <int BM, int BN, int WM, int WN, int STAGES>
 __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
@@ -301,18 +431,18 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
         __amdgpu_buffer_rsrc_t rw = make_rsrc(W0 + (size_t)t * 64);
 #pragma unroll
         for (int j = 0; j < G::A_LOADS; j++)
-            w4_dma(ra, __builtin_amdgcn_readfirstlane(st + (wave * G::A_LOADS + j) * 1024), a_off[j]);
+            dma_x4(ra, __builtin_amdgcn_readfirstlane(st + (wave * G::A_LOADS + j) * 1024), a_off[j]);
 #pragma unroll
         for (int j = 0; j < G::W_LOADS; j++)
-            w4_dma(rw, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + (wave * G::W_LOADS + j) * 1024), w_off[j]);
+            dma_x4(rw, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + (wave * G::W_LOADS + j) * 1024), w_off[j]);
         if (wave == 0) {
             __amdgpu_buffer_rsrc_t rs = make_rsrc(S0 + (size_t)t * N * 2);
-            w4_dma(rs, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + G::W_BYTES), s_off);
+            dma_x4(rs, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + G::W_BYTES), s_off);
         } else if (wave == G::NW - 1) {
             __amdgpu_buffer_rsrc_t rx = make_rsrc(X + (size_t)t * M + m0);
-            w4_dma(rx, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + G::W_BYTES + G::S_BYTES), x_off);
+            dma_x4(rx, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + G::W_BYTES + G::S_BYTES), x_off);
             if constexpr (BM * 4 > 1024)
-                w4_dma(rx, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + G::W_BYTES + G::S_BYTES + 1024), x_off2);
+                dma_x4(rx, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + G::W_BYTES + G::S_BYTES + 1024), x_off2);
         }
     };
     f32x16_t acc[G::FM][G::FN];
@@ -334,7 +464,7 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
         if ((uint32_t)s < nk) issue(s);
 
     for (uint32_t t = 0; t < nk; t++) {
-        w4_wait_vmcnt<0>();   // two stages: everything issued so far is this stage
+        wait_vmcnt<0>();   // two stages: everything issued so far is this stage
         __syncthreads();
         if (t + STAGES - 1 < nk) issue(t + STAGES - 1);
 
@@ -491,14 +621,24 @@ __device__ __forceinline__ void dequant_int4(const t0_dequant_params& p, bool bf
 
 }  // namespace t0
 
-#define T0_W4_DECODE(WAVES, MB)                                                                  \
-    extern "C" __global__ void __launch_bounds__(WAVES * 64)                                      \
-        t0k_w4a16_decode_w##WAVES##_mb##MB(const t0_w4a16_params p) {                             \
-        t0::w4_decode<WAVES, MB>(p);                                                             \
+// t0k_w4a16_decode_t<TILES>_mb<MB>: at most 16*TILES columns per workgroup,
+// M <= 16*MB.
+#define T0_W4_DECODE(TILES, MB)                                                                  \
+    extern "C" __global__ void __launch_bounds__(64 * t0_w4_decode_waves(TILES, MB))              \
+        t0k_w4a16_decode_t##TILES##_mb##MB(const t0_w4a16_params p) {                             \
+        t0::w4_decode<TILES, MB>(p);                                                             \
     }
+T0_W4_DECODE(1, 1)
+T0_W4_DECODE(2, 1)
+T0_W4_DECODE(3, 1)
 T0_W4_DECODE(4, 1)
-T0_W4_DECODE(8, 1)
+T0_W4_DECODE(1, 2)
+T0_W4_DECODE(2, 2)
+T0_W4_DECODE(3, 2)
 T0_W4_DECODE(4, 2)
+T0_W4_DECODE(1, 4)
+T0_W4_DECODE(2, 4)
+T0_W4_DECODE(3, 4)
 T0_W4_DECODE(4, 4)
 
 #define T0_W4_PREFILL(BM, BN, WM, WN, ST)                                                        \
