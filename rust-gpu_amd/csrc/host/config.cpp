@@ -31,7 +31,8 @@ const char* last_error() { return g_last_error.c_str(); }
 // Must list exactly the T0_GEMM_BOTH(...) instances of gemm_bf16.hip.
 const std::vector<GemmInstance>& gemm_instances() {
     static const std::vector<GemmInstance> v = {
-        {256, 256, 64, 2, 2, 2}, {256, 256, 32, 2, 2, 4}, {256, 128, 64, 2, 2, 3}, {128, 256, 64, 2, 2, 3},
+        {256, 256, 64, 2, 2, 2}, {256, 256, 64, 2, 4, 2}, {256, 256, 64, 4, 2, 2}, {256, 256, 32, 2, 2, 4},
+        {256, 256, 32, 2, 4, 4}, {256, 128, 64, 2, 2, 3}, {128, 256, 64, 2, 2, 3},
         {128, 128, 64, 2, 2, 4}, {128, 128, 32, 2, 2, 4}, {128, 64, 64, 2, 2, 4},  {64, 128, 64, 2, 2, 4},
         {64, 64, 64, 1, 1, 4},   {32, 64, 64, 1, 1, 6},   {32, 128, 64, 1, 2, 4},
         {32, 64, 16, 1, 1, 4},   {32, 64, 32, 1, 1, 4},   {32, 128, 16, 1, 1, 4},

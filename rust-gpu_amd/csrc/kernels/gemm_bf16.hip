@@ -116,6 +116,29 @@ T0_DEV void store_quad(const t0_gemm_params& p, uint8_t* Cb, uint32_t m, uint32_
 template <class G>
 T0_DEV void emit_rowblock(const t0_gemm_params& p, uint8_t* Cb, const float* wreg,
                           uint32_t row0, uint32_t col0, uint32_t lane) {
+    // Interior block, no epilogue chain, 16-byte aligned rows: 8 columns per
+    // lane, one 16-byte bf16 store (or two f32 stores), fully unrolled.
+    const bool bf16_out = p.flags & T0_GEMM_OUT_BF16;
+    if (p.epi_ops == 0 && row0 + 32 <= p.M && col0 + G::TN <= p.N && (p.ldc & (bf16_out ? 7u : 3u)) == 0) {
+        constexpr uint32_t LPR = G::TN / 8;            // lanes per row
+        constexpr uint32_t RPI = 64 / LPR;             // rows per iteration
+        const uint32_t rr = lane / LPR, c8 = (lane % LPR) * 8;
+#pragma unroll
+        for (uint32_t r = rr; r < 32; r += RPI) {
+            const LDS_AS float* src = (const LDS_AS float*)wreg + r * G::EPI_LD + c8;
+            const f32x4_t v0 = *(const LDS_AS f32x4_t*)src;
+            const f32x4_t v1 = *(const LDS_AS f32x4_t*)(src + 4);
+            const size_t idx = (size_t)(row0 + r) * p.ldc + col0 + c8;
+            if (bf16_out) {
+                *(u32x4_t*)((uint16_t*)Cb + idx) = u32x4_t{pack2_bf16_rne(v0[0], v0[1]), pack2_bf16_rne(v0[2], v0[3]),
+                                                           pack2_bf16_rne(v1[0], v1[1]), pack2_bf16_rne(v1[2], v1[3])};
+            } else {
+                *(f32x4_t*)((float*)Cb + idx) = v0;
+                *(f32x4_t*)((float*)Cb + idx + 4) = v1;
+            }
+        }
+        return;
+    }
     constexpr uint32_t QPR = G::TN / 4;  // quads per row
 #pragma unroll 1
     for (uint32_t q = lane; q < 32 * QPR; q += 64) {
@@ -190,7 +213,9 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
     }
 
     const uint32_t lds_base = (uint32_t)(uintptr_t)(LDS_AS uint8_t*)smem;
-    auto issue_stage = [&](uint32_t t) {
+    // Issues the loads q of stage t with q % nparts == part (A loads first,
+    // then B), so a stage can go out in slices between MFMA groups.
+    auto issue_stage = [&](uint32_t t, int part, int nparts) {
         const uint32_t kt = t * BK;                 // k offset within the partition
         const uint32_t st = lds_base + (t % STAGES) * G::STAGE_BYTES;
         const bool tail = kt + BK > k_len;
@@ -198,12 +223,14 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
         __amdgpu_buffer_rsrc_t rb = make_rsrc(NN ? B0 + (size_t)kt * ldb * 2 : B0 + (size_t)kt * 2);
 #pragma unroll
         for (int j = 0; j < G::A_LOADS; j++) {
+            if (j % nparts != part) continue;
             uint32_t off = ld.a_off[j];
             if (tail && kt + ld.a_kchunk[j] >= k_len) off = OOB_OFFSET;
             dma_x4(ra, __builtin_amdgcn_readfirstlane(st + (wave * G::A_LOADS + j) * 1024), off);
         }
 #pragma unroll
         for (int j = 0; j < G::B_LOADS; j++) {
+            if ((G::A_LOADS + j) % nparts != part) continue;
             uint32_t off = ld.b_off[j];
             if (tail && kt + ld.b_krow[j] >= k_len) off = OOB_OFFSET;
             dma_x4(rb, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + (wave * G::B_LOADS + j) * 1024), off);
@@ -246,13 +273,17 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
     // prologue
 #pragma unroll
     for (int s = 0; s < STAGES - 1; s++)
-        if ((uint32_t)s < nk) issue_stage(s);
+        if ((uint32_t)s < nk) issue_stage(s, 0, 1);
 
     for (uint32_t t = 0; t < nk; t++) {
         if (t + STAGES - 2 < nk) wait_vmcnt<G::LOADS * (STAGES - 2)>();
         else wait_vmcnt<0>();
         __syncthreads();
-        if (t + STAGES - 1 < nk) issue_stage(t + STAGES - 1);
+        const bool prefetch = t + STAGES - 1 < nk;
+        // one wave per SIMD: the whole next stage goes out now; two waves per
+        // SIMD: in BK/16 slices, one after each k step's MFMAs (below)
+        if constexpr (G::NW < 8)
+            if (prefetch) issue_stage(t + STAGES - 1, 0, 1);
 
         const LDS_AS uint8_t* sa = (const LDS_AS uint8_t*)smem + (t % STAGES) * G::STAGE_BYTES;
         const LDS_AS uint8_t* sb = sa + G::A_BYTES;
@@ -280,14 +311,33 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
         for (int kk = 0; kk < BK / 16; kk++) {
             const int cur = kk & 1;
             if (kk + 1 < BK / 16) load_frags(kk + 1, af[cur ^ 1], bfr[cur ^ 1]);
-            // keep the next step's LDS reads ahead of this step's MFMAs (the
-            // scheduler would otherwise sink them next to their uses)
-            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (G::NW < 8) {
+                // one wave per SIMD: all of the next step's LDS reads go ahead
+                // of this step's MFMAs (the scheduler would otherwise sink
+                // them next to their uses)
+                __builtin_amdgcn_sched_barrier(0);
+            }
 #pragma unroll
             for (int i = 0; i < G::FM; i++)
 #pragma unroll
                 for (int j = 0; j < G::FN; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[cur][j], af[cur][i], acc[i][j], 0, 0, 0);
+            if constexpr (G::NW >= 8) {
+                // two waves per SIMD: one LDS read between consecutive MFMAs,
+                // so the LDS pipe stays busy under the matrix core
+                if (kk + 1 < BK / 16) {
+                    constexpr int NR = G::FM + (NN ? 2 : 1) * G::FN;
+                    constexpr int REST = G::FM * G::FN - NR;
+#pragma unroll
+                    for (int q = 0; q < NR; q++) {
+                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                    }
+                    if constexpr (REST > 0) __builtin_amdgcn_sched_group_barrier(0x008, REST, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                if (prefetch) issue_stage(t + STAGES - 1, kk, BK / 16);
+            }
         }
     }
 
@@ -368,7 +418,10 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
 
 // gfx950-native tiles (auto-selection targets); stages = LDS buffers in flight
 T0_GEMM_BOTH(256, 256, 64, 2, 2, 2)
+T0_GEMM_BOTH(256, 256, 64, 2, 4, 2)
+T0_GEMM_BOTH(256, 256, 64, 4, 2, 2)
 T0_GEMM_BOTH(256, 256, 32, 2, 2, 4)
+T0_GEMM_BOTH(256, 256, 32, 2, 4, 4)
 T0_GEMM_BOTH(256, 128, 64, 2, 2, 3)
 T0_GEMM_BOTH(128, 256, 64, 2, 2, 3)
 T0_GEMM_BOTH(128, 128, 64, 2, 2, 4)
