@@ -270,73 +270,106 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
         for (int kk = 0; kk < BK / 16; kk++) b_kk[kk] = b_lane + (((kk * 2 + hi) ^ a_swz) * 16);
     }
 
-    // prologue
-#pragma unroll
-    for (int s = 0; s < STAGES - 1; s++)
-        if ((uint32_t)s < nk) issue_stage(s, 0, 1);
-
-    for (uint32_t t = 0; t < nk; t++) {
-        if (t + STAGES - 2 < nk) wait_vmcnt<G::LOADS * (STAGES - 2)>();
-        else wait_vmcnt<0>();
-        __syncthreads();
-        const bool prefetch = t + STAGES - 1 < nk;
-        // one wave per SIMD: the whole next stage goes out now; two waves per
-        // SIMD: in BK/16 slices, one after each k step's MFMAs (below)
-        if constexpr (G::NW < 8)
-            if (prefetch) issue_stage(t + STAGES - 1, 0, 1);
-
-        const LDS_AS uint8_t* sa = (const LDS_AS uint8_t*)smem + (t % STAGES) * G::STAGE_BYTES;
+    // ---- K loop -------------------------------------------------------------
+    // Every buffer is filled up front.  Step t computes from buffer
+    // t % STAGES in BK/16 sub-steps whose operand fragments are
+    // double-buffered in registers.  In the last sub-step of step t, once its
+    // fragments are in registers, the workgroup waits for stage t+1,
+    // synchronises, refills buffer t % STAGES with stage t+STAGES and reads
+    // the first fragments of step t+1, so the barrier and the first LDS reads
+    // of a step run under the MFMAs of the previous one.
+    constexpr int KK = BK / 16;
+    auto stage_ptr = [&](uint32_t t) { return (const LDS_AS uint8_t*)smem + (t % STAGES) * G::STAGE_BYTES; };
+    auto load_frags = [&](const LDS_AS uint8_t* sa, int kk, bf16x8_t* af, bf16x8_t* bfr) {
         const LDS_AS uint8_t* sb = sa + G::A_BYTES;
-        // operand fragments of one 16-deep k step, double-buffered in
-        // registers: step kk+1 is read from LDS while step kk's MFMAs run
-        auto load_frags = [&](int kk, bf16x8_t* af, bf16x8_t* bfr) {
 #pragma unroll
-            for (int i = 0; i < G::FM; i++)
-                af[i] = *(const LDS_AS bf16x8_t*)(sa + a_kk[kk] + i * 32 * (BK * 2));
+        for (int i = 0; i < G::FM; i++)
+            af[i] = *(const LDS_AS bf16x8_t*)(sa + a_kk[kk] + i * 32 * (BK * 2));
 #pragma unroll
-            for (int j = 0; j < G::FN; j++) {
-                if constexpr (NN) {
-                    const LDS_AS uint8_t* p0 = sb + b_col[j] + kk * 16 * (BN * 2);
-                    bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((LDS_AS bf16x4_t*)p0);
-                    bf16x4_t hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((LDS_AS bf16x4_t*)(p0 + 4 * (BN * 2)));
-                    bfr[j] = __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
-                } else {
-                    bfr[j] = *(const LDS_AS bf16x8_t*)(sb + b_kk[kk] + j * 32 * (BK * 2));
-                }
+        for (int j = 0; j < G::FN; j++) {
+            if constexpr (NN) {
+                const LDS_AS uint8_t* p0 = sb + b_col[j] + kk * 16 * (BN * 2);
+                bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((LDS_AS bf16x4_t*)p0);
+                bf16x4_t hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((LDS_AS bf16x4_t*)(p0 + 4 * (BN * 2)));
+                bfr[j] = __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
+            } else {
+                bfr[j] = *(const LDS_AS bf16x8_t*)(sb + b_kk[kk] + j * 32 * (BK * 2));
             }
-        };
-        bf16x8_t af[2][G::FM], bfr[2][G::FN];
-        load_frags(0, af[0], bfr[0]);
+        }
+    };
+    auto mfmas = [&](const bf16x8_t* af, const bf16x8_t* bfr) {
 #pragma unroll
-        for (int kk = 0; kk < BK / 16; kk++) {
-            const int cur = kk & 1;
-            if (kk + 1 < BK / 16) load_frags(kk + 1, af[cur ^ 1], bfr[cur ^ 1]);
-            if constexpr (G::NW < 8) {
-                // one wave per SIMD: all of the next step's LDS reads go ahead
-                // of this step's MFMAs (the scheduler would otherwise sink
-                // them next to their uses)
-                __builtin_amdgcn_sched_barrier(0);
+        for (int i = 0; i < G::FM; i++)
+#pragma unroll
+            for (int j = 0; j < G::FN; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
+    };
+    // keeps this sub-step's LDS reads (and DMA) ahead of its MFMAs: all of
+    // them first with one wave per SIMD (the scheduler would otherwise sink
+    // them next to their uses), one read per MFMA with two waves per SIMD
+    auto order_substep = [&]() {
+        if constexpr (G::NW < 8) {
+            __builtin_amdgcn_sched_barrier(0);
+        } else {
+            constexpr int NR = G::FM + (NN ? 2 : 1) * G::FN;
+            constexpr int REST = G::FM * G::FN - NR;
+#pragma unroll
+            for (int q = 0; q < NR; q++) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
             }
+            if constexpr (REST > 0) __builtin_amdgcn_sched_group_barrier(0x008, REST, 0);
+        }
+    };
+
+    // prologue: every buffer, then stage 0 visible and its first fragments
 #pragma unroll
-            for (int i = 0; i < G::FM; i++)
+    for (int s = 0; s < STAGES; s++)
+        if ((uint32_t)s < nk) issue_stage(s, 0, 1);
+    if (nk >= STAGES) wait_vmcnt<G::LOADS * (STAGES - 1)>();
+    else wait_vmcnt<0>();
+    __syncthreads();
+    bf16x8_t af[2][G::FM], bfr[2][G::FN];
+    if (nk) load_frags(stage_ptr(0), 0, af[0], bfr[0]);
+
+    if constexpr (KK % 2 == 0) {
+        for (uint32_t t = 0; t < nk; t++) {
+            const LDS_AS uint8_t* sa = stage_ptr(t);
 #pragma unroll
-                for (int j = 0; j < G::FN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[cur][j], af[cur][i], acc[i][j], 0, 0, 0);
-            if constexpr (G::NW >= 8) {
-                // two waves per SIMD: one LDS read between consecutive MFMAs,
-                // so the LDS pipe stays busy under the matrix core
-                if (kk + 1 < BK / 16) {
-                    constexpr int NR = G::FM + (NN ? 2 : 1) * G::FN;
-                    constexpr int REST = G::FM * G::FN - NR;
-#pragma unroll
-                    for (int q = 0; q < NR; q++) {
-                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
-                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                    }
-                    if constexpr (REST > 0) __builtin_amdgcn_sched_group_barrier(0x008, REST, 0);
+            for (int kk = 0; kk < KK; kk++) {
+                const int cur = kk & 1;
+                if (kk + 1 < KK) {
+                    load_frags(sa, kk + 1, af[cur ^ 1], bfr[cur ^ 1]);
+                } else if (t + 1 < nk) {
+                    // stage t+1 has landed once only the stages issued after
+                    // it (t+2 .. t+STAGES-1) may still be in flight
+                    if (t + STAGES - 1 < nk) wait_vmcnt<G::LOADS * (STAGES - 2)>();
+                    else wait_vmcnt<0>();
+                    __syncthreads();   // all waves are done reading buffer t % STAGES
+                    if (t + STAGES < nk) issue_stage(t + STAGES, 0, 1);
+                    load_frags(stage_ptr(t + 1), 0, af[cur ^ 1], bfr[cur ^ 1]);
                 }
-                __builtin_amdgcn_sched_barrier(0);
-                if (prefetch) issue_stage(t + STAGES - 1, kk, BK / 16);
+                mfmas(af[cur], bfr[cur]);
+                order_substep();
+            }
+        }
+    } else {
+        // one sub-step per stage (BK == 16): the fragment buffer parity
+        // alternates with the step, so steps go in pairs
+        for (uint32_t t = 0; t < nk; t += 2) {
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const uint32_t tt = t + h;
+                if (tt >= nk) break;
+                if (tt + 1 < nk) {
+                    if (tt + STAGES - 1 < nk) wait_vmcnt<G::LOADS * (STAGES - 2)>();
+                    else wait_vmcnt<0>();
+                    __syncthreads();
+                    if (tt + STAGES < nk) issue_stage(tt + STAGES, 0, 1);
+                    load_frags(stage_ptr(tt + 1), 0, af[h ^ 1], bfr[h ^ 1]);
+                }
+                mfmas(af[h], bfr[h]);
+                order_substep();
             }
         }
     }
