@@ -144,7 +144,10 @@ static bool preset(int id, t0_gemm_config* o) {
 // gfx950 (MI355X): 256 CUs, 4 SIMDs each, 1024 bf16 FLOP/cycle/SIMD dense,
 // 2.4 GHz, 160 KiB LDS/CU, 512 VGPRs per lane at one wave per SIMD.
 namespace hw {
-constexpr double CUS = 256, CLK = 2.4e9, FLOP_CU_CYC = 4096, HBM = 6.0e12, L2 = 24e12;
+// L2 is the effective L2->CU rate for operand re-reads (MI355X tile sweeps:
+// 128x4096x4096 NN ranks right at <= 16 TB/s, 4096^3 sustains ~10 TB/s of
+// re-reads under MFMA load).
+constexpr double CUS = 256, CLK = 2.4e9, FLOP_CU_CYC = 4096, HBM = 6.0e12, L2 = 16e12;
 constexpr double LDS = 160 * 1024;
 }
 
@@ -195,10 +198,14 @@ std::vector<Candidate> rank_candidates(uint32_t m, uint32_t n, uint32_t k, uint3
             const double lds_b = padded * ((tm + tn) / (tm * tn) + ((double)g.bm + g.bn) / ((double)g.bm * g.bn));
             const double t_lds = lds_b / (hw::CUS * 128.0 * hw::CLK * std::max(busy_frac, 1e-3));
             double hbm = (double)m * k * 2 + (double)n * k * 2 + (double)m * n * ob;
-            if (sk > 1) hbm += 2.0 * sk * tiles * g.bm * g.bn * 4;  // partial planes out + back
+            // partial planes: written through, read back mostly from the MALL
+            if (sk > 1) hbm += 1.0 * sk * tiles * g.bm * g.bn * 4;
             const double l2 = (double)m * k * 2 * std::ceil((double)n / g.bn) + (double)n * k * 2 * std::ceil((double)m / g.bm);
             // each round pays the pipeline fill (first tiles from HBM) ~1 us
-            const double t = std::max({t_compute, t_lds, hbm / hw::HBM, l2 / hw::L2}) + 1e-6 * rounds + 2e-6 +
+            // the bounds overlap only partly: a twentieth of the compute time
+            // shows even when memory bounds the tile
+            const double t = std::max({t_compute, t_lds, hbm / hw::HBM, l2 / hw::L2}) + 0.05 * t_compute +
+                             1e-6 * rounds + 2e-6 +
                              (sk > 1 ? 1e-6 : 0.0);
             t0_gemm_config c = mk(g.bm, g.bn, g.bk, g.threads(), true, true, 1, false);
             c.split_k = sk > 1 ? sk : 0;

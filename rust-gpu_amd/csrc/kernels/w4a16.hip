@@ -369,7 +369,10 @@ struct W4Cfg {
     static constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
     static constexpr int A_BYTES = BM * 256;
     static constexpr int W_BYTES = BN * 64;
-    static constexpr int S_BYTES = 1024;                 // BN*2 <= 1024
+    // The scale DMA writes all 64 lanes x 16 B (1 KB, lanes past BN*2 bytes
+    // write zeros), the zero-point DMA 64 x 4 B: separate slots.
+    static constexpr int S_BYTES = 2048;                 // scales [0, 1024), zero-point words [1024, 1280)
+    static constexpr int Z_OFF = 1024;
     static constexpr int X_BYTES = (BM * 4 + 1023) / 1024 * 1024;
     static constexpr int STAGE = A_BYTES + W_BYTES + S_BYTES + X_BYTES;
     static constexpr int A_LOADS = A_BYTES / (1024 * NW);
@@ -378,7 +381,8 @@ struct W4Cfg {
     static constexpr int SMEM = (STAGE * STAGES > NW * 32 * EPI_LD * 4) ? STAGE * STAGES : NW * 32 * EPI_LD * 4;
     static_assert(A_LOADS >= 1 && A_LOADS * 1024 * NW == A_BYTES, "A split");
     static_assert(W_LOADS >= 1 && W_LOADS * 1024 * NW == W_BYTES, "W split");
-    static_assert(BN * 2 <= 1024 && BM * 4 <= 1024 * 2, "S/X slots");
+    static_assert(BN * 2 <= Z_OFF && BM * 4 <= 1024 * 2, "S/Z/X slots");
+    static_assert(NW >= 3, "S, Z and X DMAs go out from three different waves");
     static_assert(SMEM <= 160 * 1024, "LDS");
     static_assert(NW >= 2 && STAGES == 2, "scale/X DMA split over two waves; vmcnt(0) per stage");
 };
@@ -421,6 +425,7 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
         w_off[j] = (n0 + r < N) ? r * (K / 2) + lc * 16 : OOB_OFFSET;
     }
     const uint32_t s_off = (lane * 16 < BN * 2 && n0 + lane * 8 < N) ? lane * 16 : OOB_OFFSET;
+    const uint32_t z_off = (lane < BN / 8 && n0 + lane * 8 < N) ? lane * 4 : OOB_OFFSET;   // zero-point word per lane
     const uint32_t x_off = (lane * 16 < BM * 4 && m0 + lane * 4 < M) ? lane * 16 : OOB_OFFSET;
     const uint32_t x_off2 = (1024 + lane * 16 < BM * 4 && m0 + 256 + lane * 4 < M) ? 1024 + lane * 16 : OOB_OFFSET;
     const uint32_t lds_base = (uint32_t)(uintptr_t)(LDS_AS uint8_t*)smem;
@@ -438,6 +443,11 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
         if (wave == 0) {
             __amdgpu_buffer_rsrc_t rs = make_rsrc(S0 + (size_t)t * N * 2);
             dma_x4(rs, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + G::W_BYTES), s_off);
+        } else if (wave == 1) {
+            if (p.zeros) {
+                __amdgpu_buffer_rsrc_t rz = make_rsrc(p.zeros + (size_t)t * (N / 8) + n0 / 8);
+                dma_x1(rz, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + G::W_BYTES + G::Z_OFF), z_off);
+            }
         } else if (wave == G::NW - 1) {
             __amdgpu_buffer_rsrc_t rx = make_rsrc(X + (size_t)t * M + m0);
             dma_x4(rx, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + G::W_BYTES + G::S_BYTES), x_off);
@@ -472,6 +482,7 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
         const LDS_AS uint8_t* sa = st;
         const LDS_AS uint8_t* sw = st + G::A_BYTES;
         const LDS_AS uint16_t* ss = (const LDS_AS uint16_t*)(st + G::A_BYTES + G::W_BYTES);
+        const LDS_AS uint32_t* sz = (const LDS_AS uint32_t*)(st + G::A_BYTES + G::W_BYTES + G::Z_OFF);
         const LDS_AS float* sx = (const LDS_AS float*)(st + G::A_BYTES + G::W_BYTES + G::S_BYTES);
 
         // this lane's W words and zero-point adders for the group
@@ -483,7 +494,8 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
             const LDS_AS uint8_t* wr = sw + col * 64;
             wlo[j] = *(const LDS_AS u32x4_t*)(wr + w_c0);
             whi[j] = *(const LDS_AS u32x4_t*)(wr + w_c1);
-            kadd[j] = kadd_of(zero_of(p, t, n0 + col < N ? n0 + col : 0));
+            const uint32_t z = p.zeros ? (sz[col / 8] >> (4 * (col % 8))) & 0xFu : p.zero_const;
+            kadd[j] = kadd_of(z);
         }
         f32x16_t tmp[G::FM][G::FN];
 #pragma unroll
