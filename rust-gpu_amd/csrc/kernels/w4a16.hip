@@ -659,6 +659,7 @@ T0_W4_DECODE(4, 4)
         t0::w4_prefill<BM, BN, WM, WN, ST>(p);                                                   \
     }
 T0_W4_PREFILL(256, 128, 2, 2, 2)
+T0_W4_PREFILL(256, 128, 4, 2, 2)
 T0_W4_PREFILL(128, 128, 2, 2, 2)
 
 extern "C" __global__ void __launch_bounds__(256) t0k_w4a16_rowsum(const t0_w4a16_params p) { t0::w4_rowsum(p); }
