@@ -366,6 +366,28 @@ int t0_copy_device(t0_runtime* rt, uint64_t src, uint64_t dst, uint64_t bytes);
 /* t0_unpad_2d (src/t0/math.rs): out[m][n] = padded[m][n_pad]. */
 int t0_unpad_2d(t0_runtime* rt, uint64_t padded, uint64_t out, uint32_t m, uint32_t n, uint32_t n_pad);
 
+/* ----------------------------------------------------- Ignis bf16 matmul */
+/* The GEMM calls of src/ignis/ops/bf16_matmul.rs on dense row-major f32
+ * device buffers, f32 output, operands rounded to bf16 (RNE) on the GPU.
+ * Any m, k, n >= 1.  The bf16 operands are staged in a buffer the runtime
+ * owns and grows on demand (hipMalloc on growth only); calls on one runtime
+ * run in its stream order and share that buffer.
+ *
+ * Y[m,n] = X[m,k] . W[k,n]  -- matmul forward, bf16_matmul.rs:33-47 with
+ * dispatch_gemm_forward :162-207 (W is read as the NN operand, not transposed). */
+int t0_bf16_matmul(t0_runtime* rt, uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t k, uint32_t n);
+/* dX[m,k] = dY[m,n] . W[k,n]^T  -- gemm_backward_data, bf16_matmul.rs:215-258. */
+int t0_bf16_matmul_backward_data(t0_runtime* rt, uint64_t dy, uint64_t w, uint64_t dx, uint32_t m, uint32_t k,
+                                 uint32_t n);
+/* dW[k,n] = X[m,k]^T . dY[m,n]  -- gemm_backward_weight, bf16_matmul.rs:265-308
+ * (X^T is produced by the converting kernel; dY is not transposed). */
+int t0_bf16_matmul_backward_weight(t0_runtime* rt, uint64_t x, uint64_t dy, uint64_t dw, uint32_t m, uint32_t k,
+                                   uint32_t n);
+/* Y[m,n] = X[m,k] . WT[n,k]^T with WT dense bf16  -- matmul_with_wt_bf16,
+ * bf16_matmul.rs:102-134. */
+int t0_bf16_matmul_with_wt_bf16(t0_runtime* rt, uint64_t x, uint64_t wt, uint64_t y, uint32_t m, uint32_t k,
+                                uint32_t n);
+
 #ifdef __cplusplus
 }
 #endif

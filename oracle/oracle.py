@@ -171,6 +171,28 @@ def gemm_f64(a: np.ndarray, b: np.ndarray, layout: str) -> np.ndarray:
     return y
 
 
+def bf16_matmul(x: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """Ignis matmul forward: Y[M,N] = bf16(X[M,K]) . bf16(W[K,N]) in f32.
+    Ref: src/ignis/ops/bf16_matmul.rs:162-207 (X converted with RNE at
+    :370-373, W converted and transposed at :407-414, NT GEMM).  Zero padding
+    of the reference adds exact zeros, so the product is the unpadded one."""
+    return gemm_nn(bf16_rne(np.asarray(x, np.float32)), bf16_rne(np.asarray(w, np.float32)))
+
+
+def bf16_matmul_backward_data(dy: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """dX[M,K] = bf16(dY[M,N]) . bf16(W[K,N])^T.
+    Ref: src/ignis/ops/bf16_matmul.rs:215-258 (W is the NT operand as stored)."""
+    return gemm_nt(bf16_rne(np.asarray(dy, np.float32)), bf16_rne(np.asarray(w, np.float32)))
+
+
+def bf16_matmul_backward_weight(x: np.ndarray, dy: np.ndarray) -> np.ndarray:
+    """dW[K,N] = bf16(X[M,K])^T . bf16(dY[M,N]).
+    Ref: src/ignis/ops/bf16_matmul.rs:265-308 (X^T and dY^T built by the CPU
+    transpose-convert :389-423, then NT GEMM over the contraction M)."""
+    xt = bf16_rne(np.ascontiguousarray(np.asarray(x, np.float32).T))
+    return gemm_nn(xt, bf16_rne(np.asarray(dy, np.float32)))
+
+
 def splitk_sum(planes: np.ndarray) -> np.ndarray:
     """Host split-K plane sum. Ref: examples/hello_gemm_gen.rs:125-136."""
     planes = np.ascontiguousarray(planes, dtype=np.float32)

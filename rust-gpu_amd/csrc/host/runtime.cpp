@@ -63,6 +63,8 @@ struct t0_runtime {
     std::map<size_t, std::vector<t0_buffer*>> pool;
     void* ws = nullptr;
     size_t ws_bytes = 0;
+    void* stage = nullptr;          // bf16 operand staging of the matmul path
+    size_t stage_bytes = 0;
     uint32_t* sem = nullptr;
     size_t sem_count = 0;
     uint32_t slot = 0;
@@ -113,6 +115,15 @@ int ensure_ws(t0_runtime* rt, size_t bytes) {
     return T0_OK;
 }
 
+int ensure_stage(t0_runtime* rt, size_t bytes) {
+    if (bytes <= rt->stage_bytes) return T0_OK;
+    if (rt->stage) { HIPCHK(hipStreamSynchronize(rt->stream)); HIPCHK(hipFree(rt->stage)); rt->stage = nullptr; rt->stage_bytes = 0; }
+    size_t want = std::max<size_t>(bytes + 4096, 16u << 20);
+    HIPCHK(hipMalloc(&rt->stage, want));
+    rt->stage_bytes = want;
+    return T0_OK;
+}
+
 int ensure_sem(t0_runtime* rt, size_t count) {
     if (count <= rt->sem_count) return T0_OK;
     if (rt->sem) { HIPCHK(hipStreamSynchronize(rt->stream)); HIPCHK(hipFree(rt->sem)); rt->sem = nullptr; rt->sem_count = 0; }
@@ -126,20 +137,22 @@ int ensure_sem(t0_runtime* rt, size_t count) {
 
 bool aligned16(uint64_t p) { return (p & 15) == 0; }
 
-// Fast tiled kernels need 16-byte rows; anything else takes the generic kernel.
-bool fast_ok(const t0_gemm_params& p, bool nn, bool out_bf16) {
+// Fast tiled kernels need 16-byte operand rows; anything else takes the
+// generic kernel.  NN reads B in 8-column chunks: with N % 8 != 0 the last
+// chunk of a row runs past column N, which stays inside the row only when the
+// caller guarantees ldb >= round_up(N, 8) allocated columns (b_cols_padded).
+bool fast_ok(const t0_gemm_params& p, bool nn, bool b_cols_padded = false) {
     if (!aligned16((uint64_t)p.A) || !aligned16((uint64_t)p.B) || !aligned16((uint64_t)p.C)) return false;
-    if (p.lda % 8 || p.ldb % 8 || p.ldc % 4) return false;
+    if (p.lda % 8 || p.ldb % 8) return false;
     if (p.K % (8 * p.split_k)) return false;
-    if (nn && p.N % 8) return false;
-    (void)out_bf16;
+    if (nn && p.N % 8 && !(b_cols_padded && p.ldb >= (p.N + 7) / 8 * 8)) return false;
     return true;
 }
 
-int run_gemm_params(t0_runtime* rt, const GemmInstance* g, bool nn, t0_gemm_params& p, uint32_t threads_override = 0) {
-    const bool out_bf16 = p.flags & T0_GEMM_OUT_BF16;
+int run_gemm_params(t0_runtime* rt, const GemmInstance* g, bool nn, t0_gemm_params& p, uint32_t threads_override = 0,
+                    bool b_cols_padded = false) {
     hipFunction_t f;
-    if (!g || !fast_ok(p, nn, out_bf16)) {
+    if (!g || !fast_ok(p, nn, b_cols_padded)) {
         if (p.flags & T0_GEMM_FIXUP) {   // generic kernel writes planes; reduce separately
             return fail(T0_ERR_INVALID, "in-kernel split-K needs the tiled path (16-byte aligned rows)");
         }
@@ -277,6 +290,7 @@ int t0_runtime_destroy(t0_runtime* rt) {
     for (auto& kv : rt->pool)
         for (auto* b : kv.second) { hipFree(b->ptr); delete b; }
     if (rt->ws) hipFree(rt->ws);
+    if (rt->stage) hipFree(rt->stage);
     if (rt->sem) hipFree(rt->sem);
     if (rt->module) hipModuleUnload(rt->module);
     if (rt->own_stream) hipStreamDestroy(rt->own_stream);
@@ -756,7 +770,7 @@ int t0_gemm(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm_desc* d) {
     if (r) return r;
     r = set_dev(rt);
     if (r) return r;
-    if (p.split_k > 1 && !fast_ok(p, d->transpose == T0_NN, false)) p.split_k = 1, p.flags &= ~T0_GEMM_FIXUP;
+    if (p.split_k > 1 && !fast_ok(p, d->transpose == T0_NN)) p.split_k = 1, p.flags &= ~T0_GEMM_FIXUP;
     return run_gemm_params(rt, g, d->transpose == T0_NN, p);
 }
 
@@ -1203,6 +1217,138 @@ int t0_unpad_2d(t0_runtime* rt, uint64_t padded, uint64_t out, uint32_t m, uint3
     p.src = (const void*)padded; p.dst = (void*)out;
     p.m = m; p.n = n; p.ld_src = n_pad; p.ld_dst = n;
     return launch(rt, f, (uint32_t)(((uint64_t)m * n + 255) / 256), 1, 1, 256, p);
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------ bf16 matmul path --
+// src/ignis/ops/bf16_matmul.rs converts f32 operands to bf16 on the CPU,
+// transposes W / X / dY on the CPU and pads every dimension to the tile.
+// Here each operand is converted once by a GPU kernel into the runtime's
+// staging buffer, with rows padded to 8 elements (zeros) so that the tiled
+// kernels apply at any m / k / n; the output is written straight into the
+// caller's dense f32 buffer (no padded output, no unpad pass).
+namespace {
+
+uint32_t round8(uint32_t x) { return (x + 7u) & ~7u; }
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// dst[rows_pad][ld_dst] bf16 = RNE(src[m][n] f32, row stride ld_src), zero padded.
+int stage_cvt(t0_runtime* rt, uint64_t src, uint32_t ld_src, uint32_t m, uint32_t n, uint64_t dst, uint32_t ld_dst,
+              uint32_t rows_pad) {
+    hipFunction_t f;
+    int r = get_fn(rt, "t0k_cvt_pad_bf16", &f);
+    if (r) return r;
+    t0_aux_params p;
+    memset(&p, 0, sizeof p);
+    p.src = (const void*)src; p.dst = (void*)dst;
+    p.m = m; p.n = n; p.ld_src = ld_src; p.ld_dst = ld_dst; p.rows_pad = rows_pad;
+    p.flags = (aligned16(src) && ld_src % 4 == 0) ? T0_AUX_SRC_VEC4 : 0;
+    const uint64_t chunks = (uint64_t)rows_pad * (ld_dst / 8);
+    return launch(rt, f, (uint32_t)((chunks + 255) / 256), 1, 1, 256, p);
+}
+
+// dst[rows_pad][ld_dst] bf16 = RNE(src[m][n] f32)^T, zero padded.
+int stage_cvt_t(t0_runtime* rt, uint64_t src, uint32_t ld_src, uint32_t m, uint32_t n, uint64_t dst, uint32_t ld_dst,
+                uint32_t rows_pad) {
+    hipFunction_t f;
+    int r = get_fn(rt, "t0k_cvt_t_bf16", &f);
+    if (r) return r;
+    t0_aux_params p;
+    memset(&p, 0, sizeof p);
+    p.src = (const void*)src; p.dst = (void*)dst;
+    p.m = m; p.n = n; p.ld_src = ld_src; p.ld_dst = ld_dst; p.rows_pad = rows_pad;
+    const uint64_t tiles = (uint64_t)((ld_dst + 63) / 64) * ((rows_pad + 63) / 64);
+    return launch(rt, f, (uint32_t)tiles, 1, 1, 256, p);
+}
+
+// One f32-out GEMM on staged operands, with the config t0_gemm would pick.
+int staged_gemm(t0_runtime* rt, uint64_t a, uint32_t lda, uint64_t b, uint32_t ldb, uint64_t c, uint32_t ldc,
+                uint32_t m, uint32_t n, uint32_t k, bool nn) {
+    t0_gemm_desc d;
+    memset(&d, 0, sizeof d);
+    d.a = a; d.b = b; d.c = c;
+    d.m = m; d.n = n; d.k = k;
+    d.lda = lda; d.ldb = ldb; d.ldc = ldc;
+    d.transpose = nn ? T0_NN : T0_NT;
+    d.out_dtype = T0_OUT_F32;
+    t0_gemm_config cfg;
+    int r = t0_gemm_select(rt, &d, &cfg);
+    if (r) return r;
+    const GemmInstance* g = instance_for(cfg);
+    if (!g) return fail(T0_ERR_INFEASIBLE, "%s: no gfx950 kernel", config_name(cfg).c_str());
+    t0_gemm_params p;
+    r = desc_to_params(&d, cfg, p);
+    if (r) return r;
+    if (p.split_k > 1 && !fast_ok(p, nn, true)) p.split_k = 1, p.flags &= ~T0_GEMM_FIXUP;
+    return run_gemm_params(rt, g, nn, p, 0, true);
+}
+
+int matmul_args(t0_runtime* rt, uint64_t p0, uint64_t p1, uint64_t p2, uint32_t m, uint32_t k, uint32_t n) {
+    if (!rt || !p0 || !p1 || !p2) return fail(T0_ERR_INVALID, "null argument");
+    if (!m || !k || !n) return fail(T0_ERR_INVALID, "empty matmul m=%u k=%u n=%u", m, k, n);
+    if (m > 0x7FFFFFF8u || k > 0x7FFFFFF8u || n > 0x7FFFFFF8u) return fail(T0_ERR_INVALID, "dimension too large");
+    return set_dev(rt);
+}
+
+}  // namespace
+
+extern "C" {
+
+int t0_bf16_matmul(t0_runtime* rt, uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t k, uint32_t n) {
+    int r = matmul_args(rt, x, w, y, m, k, n);
+    if (r) return r;
+    const uint32_t k8 = round8(k), n8 = round8(n);
+    const size_t a_bytes = align256((size_t)m * k8 * 2), b_bytes = align256((size_t)k8 * n8 * 2);
+    r = ensure_stage(rt, a_bytes + b_bytes);
+    if (r) return r;
+    const uint64_t sa = (uint64_t)rt->stage, sb = sa + a_bytes;
+    if ((r = stage_cvt(rt, x, k, m, k, sa, k8, m))) return r;        // X  -> [m][k8]
+    if ((r = stage_cvt(rt, w, n, k, n, sb, n8, k8))) return r;       // W  -> [k8][n8], rows k.. zero
+    return staged_gemm(rt, sa, k8, sb, n8, y, n, m, n, k8, true);    // NN: no transpose of W
+}
+
+int t0_bf16_matmul_backward_data(t0_runtime* rt, uint64_t dy, uint64_t w, uint64_t dx, uint32_t m, uint32_t k,
+                                 uint32_t n) {
+    int r = matmul_args(rt, dy, w, dx, m, k, n);
+    if (r) return r;
+    const uint32_t n8 = round8(n);
+    const size_t a_bytes = align256((size_t)m * n8 * 2), b_bytes = align256((size_t)k * n8 * 2);
+    r = ensure_stage(rt, a_bytes + b_bytes);
+    if (r) return r;
+    const uint64_t sa = (uint64_t)rt->stage, sb = sa + a_bytes;
+    if ((r = stage_cvt(rt, dy, n, m, n, sa, n8, m))) return r;       // dY -> [m][n8]
+    if ((r = stage_cvt(rt, w, n, k, n, sb, n8, k))) return r;        // W  -> [k][n8]: the NT operand as is
+    return staged_gemm(rt, sa, n8, sb, n8, dx, k, m, k, n8, false);
+}
+
+int t0_bf16_matmul_backward_weight(t0_runtime* rt, uint64_t x, uint64_t dy, uint64_t dw, uint32_t m, uint32_t k,
+                                   uint32_t n) {
+    int r = matmul_args(rt, x, dy, dw, m, k, n);
+    if (r) return r;
+    const uint32_t m8 = round8(m), n8 = round8(n);
+    const size_t a_bytes = align256((size_t)k * m8 * 2), b_bytes = align256((size_t)m8 * n8 * 2);
+    r = ensure_stage(rt, a_bytes + b_bytes);
+    if (r) return r;
+    const uint64_t sa = (uint64_t)rt->stage, sb = sa + a_bytes;
+    if ((r = stage_cvt_t(rt, x, k, m, k, sa, m8, k))) return r;      // X^T -> [k][m8]
+    if ((r = stage_cvt(rt, dy, n, m, n, sb, n8, m8))) return r;      // dY  -> [m8][n8], rows m.. zero
+    return staged_gemm(rt, sa, m8, sb, n8, dw, n, k, n, m8, true);
+}
+
+int t0_bf16_matmul_with_wt_bf16(t0_runtime* rt, uint64_t x, uint64_t wt, uint64_t y, uint32_t m, uint32_t k,
+                                uint32_t n) {
+    int r = matmul_args(rt, x, wt, y, m, k, n);
+    if (r) return r;
+    const uint32_t k8 = round8(k);
+    const size_t a_bytes = align256((size_t)m * k8 * 2);
+    r = ensure_stage(rt, a_bytes);
+    if (r) return r;
+    const uint64_t sa = (uint64_t)rt->stage;
+    if ((r = stage_cvt(rt, x, k, m, k, sa, k8, m))) return r;        // X -> [m][k8]
+    // WT is the caller's dense [n][k] bf16: the contraction stays k (a k that
+    // is not a multiple of 8 takes the generic kernel).
+    return staged_gemm(rt, sa, k8, wt, k, y, n, m, n, k, false);
 }
 
 }  // extern "C"

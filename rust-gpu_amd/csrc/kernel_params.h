@@ -90,7 +90,12 @@ typedef struct t0_aux_params {
     uint32_t planes;      // split-K plane count (reduce)
     uint32_t flags;       // T0_GEMM_OUT_BF16 for reduce output
     uint64_t plane_stride;  // bytes
+    uint32_t rows_pad;    // conversion: rows of dst written (zero past m / n)
+    uint32_t aux_pad_;
 } t0_aux_params;
+
+// t0_aux_params.flags bit for the conversions: src 16-byte aligned, ld_src % 4 == 0.
+#define T0_AUX_SRC_VEC4 0x100u
 
 #ifdef __cplusplus
 }

@@ -82,6 +82,64 @@ __device__ __forceinline__ void f32_to_bf16(const t0_aux_params& p) {
     ((uint16_t*)p.dst)[(size_t)r * p.ld_dst + c] = (uint16_t)(pack2_bf16_rne(v, 0.f) & 0xFFFFu);
 }
 
+// Operand staging for the bf16 matmul path (the CPU loops of
+// src/ignis/ops/bf16_matmul.rs:356-423 moved onto the GPU):
+//   dst[r][c] = RNE(src[r][c])  for r < m, c < n
+//             = 0               for n <= c < ld_dst or m <= r < rows_pad
+// dst is bf16 with row stride ld_dst (a multiple of 8); one lane writes one
+// 16-byte chunk of 8 elements.
+__device__ __forceinline__ void cvt_pad_bf16(const t0_aux_params& p) {
+    const uint32_t cpr = p.ld_dst / 8;
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (uint64_t)p.rows_pad * cpr) return;
+    const uint32_t r = (uint32_t)(i / cpr), c0 = (uint32_t)(i % cpr) * 8;
+    const float* s = (const float*)p.src + (size_t)r * p.ld_src + c0;
+    f32x4_t lo, hi;
+    if (r < p.m && c0 + 8 <= p.n && (p.flags & T0_AUX_SRC_VEC4)) {
+        lo = *(const f32x4_t*)s;
+        hi = *(const f32x4_t*)(s + 4);
+    } else {
+        const bool row_ok = r < p.m;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            lo[e] = (row_ok && c0 + e < p.n) ? s[e] : 0.0f;
+            hi[e] = (row_ok && c0 + 4 + e < p.n) ? s[4 + e] : 0.0f;
+        }
+    }
+    *(u32x4_t*)((uint16_t*)p.dst + (size_t)r * p.ld_dst + c0) =
+        u32x4_t{pack2_bf16_rne(lo[0], lo[1]), pack2_bf16_rne(lo[2], lo[3]),
+                pack2_bf16_rne(hi[0], hi[1]), pack2_bf16_rne(hi[2], hi[3])};
+}
+
+// Transposing variant (the X^T / dY^T of bf16_matmul.rs:389-423):
+//   dst[c][r] = RNE(src[r][c])  for r < m, c < n
+//             = 0               for m <= r < ld_dst or n <= c < rows_pad
+// src f32 [m][ld_src]; dst bf16 [rows_pad][ld_dst], ld_dst a multiple of 8.
+// A 256-lane workgroup moves one 64 x 64 tile through LDS: coalesced f32 row
+// reads, then 16-byte bf16 row writes of the transposed tile.
+__device__ __forceinline__ void cvt_t_bf16(const t0_aux_params& p) {
+    __shared__ float tile[64][65];
+    const uint32_t tiles_c = (p.rows_pad + 63) / 64;             // along src columns
+    const uint32_t r0 = (blockIdx.x / tiles_c) * 64, c0 = (blockIdx.x % tiles_c) * 64;
+    const uint32_t t = threadIdx.x;
+    const float* src = (const float*)p.src;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const uint32_t idx = t + 256 * i, r = idx / 64, c = idx % 64;
+        tile[r][c] = (r0 + r < p.m && c0 + c < p.n) ? src[(size_t)(r0 + r) * p.ld_src + c0 + c] : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const uint32_t q = t + 256 * i, cc = q / 8, rr = (q % 8) * 8;
+        if (c0 + cc >= p.rows_pad || r0 + rr >= p.ld_dst) continue;
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) w[e] = pack2_bf16_rne(tile[rr + 2 * e][cc], tile[rr + 2 * e + 1][cc]);
+        *(u32x4_t*)((uint16_t*)p.dst + (size_t)(c0 + cc) * p.ld_dst + r0 + rr) = u32x4_t{w[0], w[1], w[2], w[3]};
+    }
+}
+
 // out[m][n] = padded[m][n_pad]  (src/t0/math.rs t0_unpad_2d semantics).
 __device__ __forceinline__ void unpad_2d(const t0_aux_params& p) {
     const uint64_t e = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -97,6 +155,8 @@ extern "C" __global__ void __launch_bounds__(256) t0k_gemm_generic_nn(const t0_g
 extern "C" __global__ void __launch_bounds__(256) t0k_splitk_reduce(const t0_aux_params p) { t0::splitk_reduce(p); }
 extern "C" __global__ void __launch_bounds__(256) t0k_f32_to_bf16(const t0_aux_params p) { t0::f32_to_bf16(p); }
 extern "C" __global__ void __launch_bounds__(256) t0_unpad_2d(const t0_aux_params p) { t0::unpad_2d(p); }
+extern "C" __global__ void __launch_bounds__(256) t0k_cvt_pad_bf16(const t0_aux_params p) { t0::cvt_pad_bf16(p); }
+extern "C" __global__ void __launch_bounds__(256) t0k_cvt_t_bf16(const t0_aux_params p) { t0::cvt_t_bf16(p); }
 
 // Plain 16-byte-per-lane copy of n16 chunks: the calibration kernel whose
 // known byte count scales the FETCH_SIZE / WRITE_SIZE counters.

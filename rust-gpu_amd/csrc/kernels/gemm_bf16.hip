@@ -89,9 +89,11 @@ T0_DEV void store_quad(const t0_gemm_params& p, uint8_t* Cb, uint32_t m, uint32_
             v[e] = apply_epilogue(v[e], ops, bv, p.epi_scale, p.clamp_lo, p.clamp_hi);
         }
     }
+    // n is a multiple of 4: a quad is 8/16-byte aligned when ldc is a multiple of 4
+    const bool vec = n + 3 < N && (p.ldc & 3u) == 0;
     if (p.flags & T0_GEMM_OUT_BF16) {
         uint16_t* dst = (uint16_t*)Cb + (size_t)m * p.ldc + n;
-        if (n + 3 < N) {
+        if (vec) {
             *(u32x2_t*)dst = u32x2_t{pack2_bf16_rne(v[0], v[1]), pack2_bf16_rne(v[2], v[3])};
         } else {
 #pragma unroll
@@ -100,7 +102,7 @@ T0_DEV void store_quad(const t0_gemm_params& p, uint8_t* Cb, uint32_t m, uint32_
         }
     } else {
         float* dst = (float*)Cb + (size_t)m * p.ldc + n;
-        if (n + 3 < N) {
+        if (vec) {
             *(f32x4_t*)dst = v;
         } else {
 #pragma unroll

@@ -268,9 +268,9 @@ def test_raw_kernel_load_and_dispatch(rt, dev):
     n = 4096
     x = np.random.default_rng(2).standard_normal(n).astype(np.float32) * 100
     src, dst = dev.up(x), dev.zeros(n * 2)
-    kern = rt.kernel_load(t0.code_object(), "t0k_f32_to_bf16", [256], kernarg_size=48)
-    # t0_aux_params: src, dst, m, n, ld_src, ld_dst, planes, flags, plane_stride
-    ka = struct.pack("<QQIIIIIIQ", src, dst, 1, n, n, n, 0, 0, 0)
+    kern = rt.kernel_load(t0.code_object(), "t0k_f32_to_bf16", [256], kernarg_size=56)
+    # t0_aux_params: src, dst, m, n, ld_src, ld_dst, planes, flags, plane_stride, rows_pad, pad
+    ka = struct.pack("<QQIIIIIIQII", src, dst, 1, n, n, n, 0, 0, 0, 0, 0)
     rt.dispatch(kern, [n, 1, 1], ka)
     got = dev.down(dst, np.uint16, n)
     assert np.array_equal(got, orc.bf16_rne(x))

@@ -15,6 +15,8 @@ Pin map (function -> checks in this file):
                      all-ones, auto_gemm smoke pattern, tile_ir structured
                      pattern); NN == NT on B^T; sequential-order IEEE case
   gemm_rows          equals the full product's rows
+  bf16_matmul*       int64 products on integer inputs (forward, dX, dW, non-
+                     square); RNE tie cases that unrounded operands would fail
   splitk_sum         IEEE order case + integer planes
   int4 pack/unpack   src/t0/quant_kernels.rs:347-491 known answers
   dequant_int4_*     brute force over all (q, z) x scales vs exact product
@@ -210,6 +212,38 @@ def test_gemm_rows_slice():
     full = orc.gemm_nn(a, b)
     assert np.array_equal(orc.gemm_rows(a, b, "nn", 16, 32), full[16:32])
     assert np.array_equal(orc.gemm_rows(a, b.T.copy(), "nt", 0, 8), full[0:8])
+
+
+@pytest.mark.parametrize("m,k,n", [(3, 5, 7), (17, 40, 9), (24, 33, 65)])
+def test_bf16_matmul_integer_closed_forms(m, k, n):
+    """Ignis matmul forward / backward-data / backward-weight on small-integer
+    f32 inputs (exact in bf16, every partial sum exact) against int64 matrix
+    products.  Non-square shapes, so a swapped or transposed operand changes
+    the output shape or values."""
+    rng = np.random.default_rng(m * 1000 + k)
+    x = rng.integers(-8, 9, (m, k))
+    w = rng.integers(-8, 9, (k, n))
+    dy = rng.integers(-8, 9, (m, n))
+    y = orc.bf16_matmul(x.astype(np.float32), w.astype(np.float32))
+    assert y.shape == (m, n) and np.array_equal(y.astype(np.int64), x @ w)
+    dx = orc.bf16_matmul_backward_data(dy.astype(np.float32), w.astype(np.float32))
+    assert dx.shape == (m, k) and np.array_equal(dx.astype(np.int64), dy @ w.T)
+    dw = orc.bf16_matmul_backward_weight(x.astype(np.float32), dy.astype(np.float32))
+    assert dw.shape == (k, n) and np.array_equal(dw.astype(np.int64), x.T @ dy)
+
+
+def test_bf16_matmul_rounds_operands_rne():
+    """bf16_matmul.rs:371-372 rounds both f32 operands to nearest even before
+    the product: 1 + 2^-8 is a tie that rounds down to 1 (even), 1 + 3*2^-8 a
+    tie that rounds up to 1 + 2^-6, 1 + 2^-8 + 2^-20 rounds up to 1 + 2^-7.
+    With unrounded operands each sum would carry the extra terms."""
+    k = 16
+    ones = np.ones((k, 1), np.float32)
+    for v, want in [(1 + 2.0**-8, 1.0), (1 + 3 * 2.0**-8, 1 + 2.0**-6), (1 + 2.0**-8 + 2.0**-20, 1 + 2.0**-7)]:
+        x = np.full((1, k), v, np.float32)
+        assert orc.bf16_matmul(x, ones)[0, 0] == np.float32(k * want)
+        assert orc.bf16_matmul(ones.T.copy(), x.T.copy())[0, 0] == np.float32(k * want)
+        assert orc.bf16_matmul_backward_weight(x.T.copy(), np.ones((k, 1), np.float32))[0, 0] == np.float32(k * want)
 
 
 def test_splitk_sum():
