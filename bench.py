@@ -10,7 +10,8 @@ duration to MI355X's dense bf16 MFMA peak (2516.6 TFLOP/s); ``cpu_baseline``
 times the reference's CPU matmul (restated in oracle/, single thread) on a
 row slice of the same workload.  ``extras`` carries the other BASELINE
 configs: skinny bf16 GEMM (HBM), W4A16 decode (HBM, the metric's second
-half) and W4A16 prefill (MFMA), each with its own roofline; the HBM-bound
+half), W4A16 prefill (MFMA), each with its own roofline, and the Ignis
+f32 matmul forward / backward at 4096^3 (staging conversions + GEMM); the HBM-bound
 shapes rotate 12 weight copies (> 256 MB) so the Infinity Cache cannot
 serve them, and are timed as graph replays of 12 launches.
 """
@@ -229,6 +230,34 @@ def bench_prefill(rt, steps, warmup, rng, tr):
             "roofline": roofline("mfma", tflops, PEAK_TFLOPS, "TFLOP/s", traffic_of(tr, "w4a16_prefill_4096x4096x14336"))}
 
 
+def bench_ignis(rt, steps, warmup, rng, tr):
+    """Ignis bf16 matmul (f32 X[M,K], W[K,N] -> f32 Y) at M=N=K=4096: forward
+    (two staging conversions + NN GEMM) and backward (dX = dY W^T and
+    dW = X^T dY, four conversions + two GEMMs)."""
+    m = n = k = 4096
+    x = rt.upload(rng.standard_normal((m, k), dtype=np.float32))
+    w = rt.upload(rng.standard_normal((k, n), dtype=np.float32))
+    dy = rt.upload(rng.standard_normal((m, n), dtype=np.float32))
+    y, dx, dw = rt.alloc(m * n * 4), rt.alloc(m * k * 4), rt.alloc(k * n * 4)
+    L = t0.lib()
+
+    def fwd():
+        t0._check(L.t0_bf16_matmul(rt.h, x.gpu_addr(), w.gpu_addr(), y.gpu_addr(), m, k, n))
+
+    def bwd():
+        t0._check(L.t0_bf16_matmul_backward_data(rt.h, dy.gpu_addr(), w.gpu_addr(), dx.gpu_addr(), m, k, n))
+        t0._check(L.t0_bf16_matmul_backward_weight(rt.h, x.gpu_addr(), dy.gpu_addr(), dw.gpu_addr(), m, k, n))
+
+    ms_f = Timer(rt).run(fwd, steps, warmup)
+    ms_b = Timer(rt).run(bwd, steps, warmup)
+    for buf in (x, w, dy, y, dx, dw):
+        buf.free()
+    fl = 2.0 * m * n * k
+    return {"workload": "Ignis bf16 matmul M=N=K=4096, f32 in / f32 out", "us_forward": round(ms_f * 1e3, 2),
+            "tflops_forward": round(fl / (ms_f * 1e-3) / 1e12, 1), "us_backward": round(ms_b * 1e3, 2),
+            "tflops_backward": round(2 * fl / (ms_b * 1e-3) / 1e12, 1)}
+
+
 def cpu_baseline(a, b, rows: int):
     """The reference CPU matmul (oracle restatement, one thread) on rows
     [0, rows) of the 4096^3 product, scaled to the whole product."""
@@ -255,7 +284,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="issue rotated launches directly (for tracers)")
-    ap.add_argument("--only", choices=["gemm4096", "skinny", "decode", "prefill", "copy"], default=None,
+    ap.add_argument("--only", choices=["gemm4096", "skinny", "decode", "prefill", "ignis", "copy"], default=None,
                     help="run one workload (for counter collection)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -272,7 +301,7 @@ def main():
 
     if args.only:
         fn = {"gemm4096": bench_gemm_4096, "skinny": bench_skinny, "decode": bench_decode,
-              "prefill": bench_prefill, "copy": bench_copy}[args.only]
+              "prefill": bench_prefill, "ignis": bench_ignis, "copy": bench_copy}[args.only]
         r = fn(rt, args.steps, args.warmup, rng, tr)
         r.pop("a", None)
         r.pop("b", None)
@@ -285,7 +314,8 @@ def main():
           f"({head['kernel']})", file=sys.stderr, flush=True)
     extras = {}
     if not args.no_extras:
-        for name, fn in (("skinny", bench_skinny), ("w4a16_decode", bench_decode), ("w4a16_prefill", bench_prefill)):
+        for name, fn in (("skinny", bench_skinny), ("w4a16_decode", bench_decode), ("w4a16_prefill", bench_prefill),
+                         ("ignis_matmul", bench_ignis)):
             extras[name] = fn(rt, args.steps, args.warmup, rng, tr)
             print(f"# {name}: {json.dumps(extras[name])}", file=sys.stderr, flush=True)
     cpu = None
