@@ -39,6 +39,13 @@ T0_DEV void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
 }
+// The same wait as a compiler memory barrier: no memory access (LDS reads of
+// DMA'd data in particular) moves across it.
+template <int N>
+T0_DEV void wait_vmcnt_fence() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+}
 
 // Global (rsrc + voffset) -> LDS (m0 + lane*16, resp. m0 + lane*4) without
 // VGPR staging.  Issued as inline asm: the compiler cannot see which LDS

@@ -65,17 +65,23 @@ T0_DEV void store_out4(const t0_w4a16_params& p, uint32_t m, uint32_t n, f32x4_t
 //   over its whole K slice and, with split_k == 1, no partial sums leave the
 //   CU.  Workgroup i owns columns [c0, c1): the 4-column units of N split
 //   evenly over gridDim.x, at most 16*TILES columns.
-//   The slice is walked in passes of KP = 32/MB quant groups (128 k each).
-//   A pass first issues every load it needs, so the whole pass is in flight
-//   at once (HBM latency is the enemy at this size):
-//     A  [16*MB rows][KP*256 B]  -> LDS by buffer_load ... lds (rows >= M are
-//                                   skipped), 16-B chunks XOR-swizzled by row
-//     S  [KP][16 x 16 B]         -> LDS, scales from column c0 (bf16: c0
-//                                   rounded down to 8)
-//     Z  [KP][16 words]          -> LDS, packed zero points from word c0/8
-//     W  -> VGPRs: wave w takes groups w, w+WAVES, ... of the pass; lane l
-//           (c = l%16, h = l/16) loads, per group and tile t, the 16 bytes of
-//           column c0 + 16t + c holding k = 128g + 32h + [0, 32).
+//   Wave w owns the quant groups w, w + WAVES, w + 2*WAVES, ... of the
+//   workgroup's K slice and loads everything a group needs by itself, so no
+//   wave waits for another until the final sum:
+//     A  [16*MB rows][256 B] of the group -> the wave's own LDS slot by
+//        buffer_load ... lds (rows past M read zeros), 16-B chunks
+//        XOR-swizzled by row
+//     W  -> VGPRs: lane l (c = l%16, h = l/16) loads, per tile t, the 16 bytes
+//        of column c0 + 16t + c holding k = 128g + 32h + [0, 32)
+//     S, Z -> the same slot by 4-byte DMAs: the group's scales of columns
+//        [c0, c1) and the zero-point words holding them
+//   Groups go in rounds of SLOTS (2 where LDS allows): every load of the
+//   round is issued, group by group, before the first group is consumed.
+//   Each group issues a fixed number of loads, so an explicit vmcnt wait
+//   lets a group's LDS data be read while the later groups' loads are still
+//   in flight; the DMAs are compiler-visible (buffer-load-to-LDS builtin), so
+//   the compiler's own waits for the weight registers count them too and
+//   group j computes while group j + 1 is still arriving.
 //   Per group, v_mfma_f32_16x16x32_bf16(W, A) with W = bf16(128 + q) gives
 //   lane l T = sum_k a*(128 + q) for outputs (m = 16mb + c,
 //   n = c0 + 16t + 4h + r), r = 0..3; a ones-MFMA gives sum_k a, and
@@ -110,30 +116,27 @@ T0_DEV bf16x8_t unpack8_128(uint32_t w, uint32_t bits4300) {
 
 template <int TILES, int MB>
 struct W4DecCfg {
-    static constexpr int KP = 32 / MB;                   // quant groups per pass
     // as many waves as the per-group registers allow (16 waves: <= 128 VGPRs)
     static constexpr int WAVES = t0_w4_decode_waves(TILES, MB), NT = 64 * WAVES;
-    static constexpr int GPW = KP / WAVES;               // groups per wave per pass
-    static constexpr int RA = KP * 256;                  // A row bytes per pass
-    static constexpr int A_BYTES = 16 * MB * RA;         // 128 KB
-    static constexpr int S_OFF = A_BYTES, S_BYTES = KP * 256;
-    static constexpr int Z_OFF = S_OFF + S_BYTES, Z_BYTES = KP * 64;
-    static constexpr int SMEM = Z_OFF + Z_BYTES;
-    static constexpr int A_DMA = A_BYTES / 1024 / WAVES; // A DMA loads per wave
-    static constexpr int S_BLOCKS = KP * 16 / 64;        // S (16 B/lane) and Z (4 B/lane) DMA blocks
-    static constexpr int S_DMA = (S_BLOCKS + WAVES - 1) / WAVES;   // per wave (block i*WAVES + wave)
-    static constexpr int W_LOADS = GPW * TILES;          // weight loads per lane per pass
-    static constexpr int OUT_SLOTS = TILES * MB * 64;    // 16-byte outputs per workgroup
-    static_assert(GPW * WAVES == KP && A_DMA * WAVES * 1024 == A_BYTES, "pass split");
-    static_assert(S_BLOCKS * 64 == KP * 16, "S/Z split");
-    static_assert(W_LOADS < 64, "vmcnt range");
-    static_assert(WAVES * OUT_SLOTS * 16 <= A_BYTES, "reduction fits the A buffer");
-    static_assert(SMEM <= 160 * 1024, "LDS");
+    static constexpr int GROUP_A = 16 * MB * 256;         // A bytes of one group
+    static constexpr int A_DMA = GROUP_A / 1024;          // 4-row DMA blocks per group
+    // a wave's slot: A, then the group's scales (<= 256 B) and zero-point words (<= 64 B)
+    static constexpr int S_OFF = GROUP_A, Z_OFF = GROUP_A + 256, WAVE_SLOT = GROUP_A + 512;
+    static constexpr int SLOT_BYTES = WAVES * WAVE_SLOT;  // one group per wave
+    static constexpr int SLOTS = 2 * SLOT_BYTES <= 156 * 1024 ? 2 : 1;   // groups in flight per wave
+    static constexpr int OUT_SLOTS = TILES * MB * 64;     // 16-byte outputs per workgroup
+    static constexpr int MAX_GROUP_LOADS = A_DMA + 2 + TILES;   // VMEM ops per group: A, S, Z, W
+    static_assert(SLOTS * MAX_GROUP_LOADS < 64, "vmcnt range");
+    static_assert(SLOTS * SLOT_BYTES <= 156 * 1024, "LDS");
+    static_assert(WAVES * OUT_SLOTS * 16 <= SLOT_BYTES, "reduction fits slot 0");
+    static_assert(TILES <= 4, "scale / zero-point DMA covers 64 columns");
 };
 
 template <int TILES, int MB, bool ZP, bool SF32>
-__device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, uint8_t* smem, uint32_t* s_last) {
+__device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, LDS_AS uint8_t* slot0, LDS_AS uint8_t* slot1,
+                                               uint32_t* s_last) {
     using G = W4DecCfg<TILES, MB>;
+    typedef __attribute__((address_space(3))) void lds_void;
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t K = p.K, N = p.N, M = p.M, sk = p.split_k;
@@ -142,52 +145,33 @@ __device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, uint8_t
     const uint32_t c0 = 4 * (uint32_t)((uint64_t)wg * units / gridDim.x);
     const uint32_t c1 = 4 * (uint32_t)((uint64_t)(wg + 1) * units / gridDim.x);
     const uint32_t GP = K / 128 / sk;                   // groups in this partition
-    const uint32_t g_begin = part * GP, g_end = g_begin + GP;
-    const uint32_t sb = SF32 ? c0 : (c0 & ~7u);          // first column of the S chunks
-    const uint32_t zb = c0 / 8;                          // first word of the Z chunks
-    const uint32_t s_row = N * (SF32 ? 4 : 2), z_row = (N / 8) * 4;
+    const uint32_t g_begin = part * GP;
     const uint32_t c = lane & 15, h = lane >> 4;
+    constexpr uint32_t ES = SF32 ? 4 : 2;               // scale bytes
+    constexpr int GROUP_LOADS = G::A_DMA + 1 + (ZP ? 1 : 0) + TILES;   // VMEM ops per group: A, S, Z, W
 
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A);
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.scales);
     const __amdgpu_buffer_rsrc_t rz = make_rsrc(ZP ? (const void*)p.zeros : p.scales);
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.qweight + (size_t)c0 * (K / 8));
-    const uint32_t lds_base = (uint32_t)(uintptr_t)(LDS_AS uint8_t*)smem;
 
-    // ---- loop-invariant per-lane offsets ------------------------------------
-    // A DMA block b = wave*A_DMA + i covers LDS bytes [b KB, (b+1) KB): row r,
-    // LDS chunk cl, global chunk cl ^ (r & 15) of the pass's k range.
+    // ---- loop-invariant per-lane offsets (OOB_OFFSET: the lane reads zeros)
+    // A DMA block i of a group: rows 4i + h' (h' = lane / 16), LDS chunk c,
+    // global chunk c ^ (row & 15) of the group's 256 bytes.
     uint32_t a_off[G::A_DMA];
 #pragma unroll
     for (int i = 0; i < G::A_DMA; i++) {
-        const uint32_t pos = (wave * G::A_DMA + i) * 1024 + lane * 16;
-        const uint32_t r = pos / G::RA, cl = (pos % G::RA) / 16;
-        const uint32_t cg = (cl & ~15u) | ((cl ^ r) & 15u);
-        a_off[i] = r * p.lda * 2 + cg * 16;
+        const uint32_t row = 4 * i + h;
+        a_off[i] = row < M ? row * p.lda * 2 + ((c ^ (row & 15)) * 16) : OOB_OFFSET;
     }
-    // S / Z DMA: lane of block b = i*WAVES + wave serves group q = (b*64 + lane)/16
-    // of the pass, chunk (word) lane % 16
-    uint32_t s_off[G::S_DMA], z_off[G::S_DMA];
-#pragma unroll
-    for (int i = 0; i < G::S_DMA; i++) {
-        const uint32_t e = (i * G::WAVES + wave) * 64 + lane, q = e / 16, k16 = e % 16;
-        const uint32_t col = sb + k16 * (SF32 ? 4 : 8);
-        s_off[i] = (col < N && col < c1) ? q * s_row + (SF32 ? col * 4 : col * 2) : OOB_OFFSET;
-        z_off[i] = (ZP && zb + k16 < N / 8 && (zb + k16) * 8 < c1) ? q * z_row + (zb + k16) * 4 : OOB_OFFSET;
-    }
-    // weight rows of this lane (column c0 + 16t + c), OOB past c1
     uint32_t w_row[TILES];
 #pragma unroll
     for (int t = 0; t < TILES; t++) w_row[t] = c0 + 16 * t + c < c1 ? (16 * t + c) * (K / 2) + 16 * h : OOB_OFFSET;
-    // per-tile reads of this lane's 4 output columns n4 .. n4+3
-    uint32_t s_rd[TILES], z_rd[TILES], z_sh[TILES];
-#pragma unroll
-    for (int t = 0; t < TILES; t++) {
-        const uint32_t n4 = c0 + 16 * t + 4 * h;
-        s_rd[t] = G::S_OFF + (n4 - sb) * (SF32 ? 4 : 2);
-        z_rd[t] = G::Z_OFF + (n4 / 8 - zb) * 4;
-        z_sh[t] = 4 * (n4 % 8);
-    }
+    // scales: lane l DMAs the 4 bytes of columns c0 + 2l, +1 (bf16) or c0 + l (f32);
+    // zero points: lane l the word c0/8 + l
+    const uint32_t zb = c0 / 8;
+    const uint32_t s_lane = (SF32 ? c0 + lane : c0 + 2 * lane) < c1 ? (SF32 ? c0 + lane : c0 + 2 * lane) * ES : OOB_OFFSET;
+    const uint32_t z_lane = (ZP && lane < 9 && (zb + lane) * 8 < c1) ? (zb + lane) * 4 : OOB_OFFSET;
     const float zc_const = 128.0f + (float)p.zero_const;
     const uint32_t bits4300 = __builtin_amdgcn_mov_dpp(0x43004300u, 0xE4, 0xF, 0xF, false);  // in a VGPR
     const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, u32x4_t{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
@@ -197,68 +181,41 @@ __device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, uint8_t
 #pragma unroll
         for (int mb = 0; mb < MB; mb++) acc[t][mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
+    // groups of this wave: g_begin + wave + WAVES * j, j < nj
+    const uint32_t nj = GP > wave ? (GP - wave + G::WAVES - 1) / G::WAVES : 0;
 #pragma unroll 1
-    for (uint32_t g0 = g_begin; g0 < g_end; g0 += G::KP) {
-        const uint32_t np = min((uint32_t)G::KP, g_end - g0);   // groups in this pass
-        if (g0 != g_begin) __syncthreads();                      // previous pass done with LDS
-        // ---- 1. A, S, Z -> LDS ----------------------------------------------
+    for (uint32_t j0 = 0; j0 < nj; j0 += G::SLOTS) {
+        // ---- 1. every load of the round, group by group ----------------------
+        u32x4_t wq[G::SLOTS][TILES];
 #pragma unroll
-        for (int i = 0; i < G::A_DMA; i++) {
-            const uint32_t b = wave * G::A_DMA + i;
-            const uint32_t r = b * 1024 / G::RA;                 // wave-uniform row
-            if (r < M) {
-                const uint32_t cl = ((b * 1024) % G::RA) / 16 + lane;   // chunk of this lane
-                const bool ok = cl / 16 < np;
-                dma_x4(ra, __builtin_amdgcn_readfirstlane(lds_base + b * 1024), ok ? a_off[i] + g0 * 256 : OOB_OFFSET);
-            }
-        }
+        for (int s = 0; s < G::SLOTS; s++) {
+            const bool ok = j0 + s < nj;          // wave-uniform; a group past nj reads zeros and adds 0
+            const uint32_t g = g_begin + wave + G::WAVES * (j0 + s);
+            LDS_AS uint8_t* dst = (s == 0 ? slot0 : slot1) + wave * G::WAVE_SLOT;
 #pragma unroll
-        for (int i = 0; i < G::S_DMA; i++) {
-            const uint32_t b = i * G::WAVES + wave;
-            if (b >= (uint32_t)G::S_BLOCKS) break;               // wave-uniform
-            const bool ok = (b * 64 + lane) / 16 < np;
-            dma_x4(rs, __builtin_amdgcn_readfirstlane(lds_base + G::S_OFF + b * 1024), ok ? s_off[i] + g0 * s_row : OOB_OFFSET);
-            if (ZP) dma_x1(rz, __builtin_amdgcn_readfirstlane(lds_base + G::Z_OFF + b * 256), ok ? z_off[i] + g0 * z_row : OOB_OFFSET);
-        }
-        // ---- 2. weights -> VGPRs, in the order they are consumed ------------
-        u32x4_t wq[G::GPW][TILES];
-#pragma unroll
-        for (int j = 0; j < G::GPW; j++) {
-            const uint32_t gl = wave + G::WAVES * j;            // group within the pass
+            for (int i = 0; i < G::A_DMA; i++)           // every block, so the count per group is fixed
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void*)(dst + i * 1024), 16,
+                                                        ok && a_off[i] != OOB_OFFSET ? a_off[i] + g * 256 : OOB_OFFSET,
+                                                        0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(dst + G::S_OFF), 4,
+                                                    ok && s_lane != OOB_OFFSET ? s_lane + g * N * ES : OOB_OFFSET, 0, 0, 0);
+            if (ZP)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rz, (lds_void*)(dst + G::Z_OFF), 4,
+                                                        ok && z_lane != OOB_OFFSET ? z_lane + g * (N / 8) * 4 : OOB_OFFSET,
+                                                        0, 0, 0);
 #pragma unroll
             for (int t = 0; t < TILES; t++)
-                wq[j][t] = buffer_load_x4(rw, gl < np ? w_row[t] + (g0 + gl) * 64 : OOB_OFFSET);
+                wq[s][t] = buffer_load_x4(rw, ok && w_row[t] != OOB_OFFSET ? w_row[t] + g * 64 : OOB_OFFSET);
+            __builtin_amdgcn_sched_barrier(0);   // keep the groups' loads in consumption order
         }
-        // ---- 3. the DMAs (issued before every weight load) are done ---------
-        __builtin_amdgcn_sched_barrier(0);
-        wait_vmcnt<G::W_LOADS>();
-        __syncthreads();
-        // ---- 4. consume the groups as their weights arrive (a group past the
-        // pass read zeros everywhere and adds exactly 0; no early exit, so no
-        // load is left in flight into the next pass's registers) -----------
-        const LDS_AS uint8_t* sp = (const LDS_AS uint8_t*)smem;
+        // ---- 2. consume the groups in order: a group's LDS data is complete
+        // once only the later groups' loads are outstanding (explicit wait,
+        // also a compiler fence); its weight registers the compiler waits for --
 #pragma unroll
-        for (int j = 0; j < G::GPW; j++) {
-            const uint32_t gl = wave + G::WAVES * j;
-            f32x4_t s4[TILES], zc[TILES];
-#pragma unroll
-            for (int t = 0; t < TILES; t++) {
-                const u32x2_t lo = *(const LDS_AS u32x2_t*)(sp + s_rd[t] + gl * 256);
-                if (SF32) {
-                    const u32x2_t hi = *(const LDS_AS u32x2_t*)(sp + s_rd[t] + gl * 256 + 8);
-                    s4[t] = f32x4_t{__uint_as_float(lo[0]), __uint_as_float(lo[1]), __uint_as_float(hi[0]), __uint_as_float(hi[1])};
-                } else {
-                    s4[t] = f32x4_t{bf16_bits_to_f32(lo[0] & 0xFFFFu), bf16_bits_to_f32(lo[0] >> 16),
-                                    bf16_bits_to_f32(lo[1] & 0xFFFFu), bf16_bits_to_f32(lo[1] >> 16)};
-                }
-                if (ZP) {
-                    const uint32_t zw = *(const LDS_AS uint32_t*)(sp + z_rd[t] + gl * 64) >> z_sh[t];
-#pragma unroll
-                    for (int r = 0; r < 4; r++) zc[t][r] = 128.0f + (float)((zw >> (4 * r)) & 0xFu);
-                } else {
-                    zc[t] = f32x4_t{zc_const, zc_const, zc_const, zc_const};
-                }
-            }
+        for (int s = 0; s < G::SLOTS; s++) {
+            if (s == 0) wait_vmcnt_fence<(G::SLOTS - 1) * GROUP_LOADS>();
+            else wait_vmcnt_fence<0>();
+            const LDS_AS uint8_t* sp = (s == 0 ? slot0 : slot1) + wave * G::WAVE_SLOT;
             // activation fragments and sums of every row block, then one tile
             // at a time: unpack its weights once, use them for every row block
             bf16x8_t av[MB][4];
@@ -268,23 +225,40 @@ __device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, uint8_t
                 const uint32_t row = 16 * mb + c;
 #pragma unroll
                 for (int w = 0; w < 4; w++)
-                    av[mb][w] = *(const LDS_AS bf16x8_t*)(sp + row * G::RA + gl * 256 + (((4 * h + w) ^ c) * 16));
+                    av[mb][w] = *(const LDS_AS bf16x8_t*)(sp + row * 256 + (((4 * h + w) ^ c) * 16));
                 sa[mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int w = 0; w < 4; w++) sa[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, av[mb][w], sa[mb], 0, 0, 0);
             }
 #pragma unroll
             for (int t = 0; t < TILES; t++) {
+                const uint32_t n4 = c0 + 16 * t + 4 * h;     // this lane's columns n4 .. n4+3
+                f32x4_t s4, zc;
+                if (SF32) {
+                    const u32x4_t v = *(const LDS_AS u32x4_t*)(sp + G::S_OFF + (16 * t + 4 * h) * 4);
+                    s4 = f32x4_t{__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3])};
+                } else {
+                    const u32x2_t v = *(const LDS_AS u32x2_t*)(sp + G::S_OFF + (16 * t + 4 * h) * 2);
+                    s4 = f32x4_t{bf16_bits_to_f32(v[0] & 0xFFFFu), bf16_bits_to_f32(v[0] >> 16),
+                                 bf16_bits_to_f32(v[1] & 0xFFFFu), bf16_bits_to_f32(v[1] >> 16)};
+                }
+                if (ZP) {
+                    const uint32_t zw = *(const LDS_AS uint32_t*)(sp + G::Z_OFF + (n4 / 8 - zb) * 4) >> (4 * (n4 % 8));
+#pragma unroll
+                    for (int r = 0; r < 4; r++) zc[r] = 128.0f + (float)((zw >> (4 * r)) & 0xFu);
+                } else {
+                    zc = f32x4_t{zc_const, zc_const, zc_const, zc_const};
+                }
                 bf16x8_t wv[4];
 #pragma unroll
-                for (int w = 0; w < 4; w++) wv[w] = unpack8_128(wq[j][t][w], bits4300);
+                for (int w = 0; w < 4; w++) wv[w] = unpack8_128(wq[s][t][w], bits4300);
 #pragma unroll
                 for (int mb = 0; mb < MB; mb++) {
                     f32x4_t tt = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int w = 0; w < 4; w++) tt = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv[w], av[mb][w], tt, 0, 0, 0);
 #pragma unroll
-                    for (int r = 0; r < 4; r++) acc[t][mb][r] = fmaf(s4[t][r], fmaf(-zc[t][r], sa[mb][r], tt[r]), acc[t][mb][r]);
+                    for (int r = 0; r < 4; r++) acc[t][mb][r] = fmaf(s4[r], fmaf(-zc[r], sa[mb][r], tt[r]), acc[t][mb][r]);
                 }
             }
         }
@@ -292,7 +266,7 @@ __device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, uint8_t
 
     // ---- sum the waves, in wave order ----------------------------------------
     __syncthreads();                                     // LDS free for the reduction
-    LDS_AS f32x4_t* red = (LDS_AS f32x4_t*)(LDS_AS uint8_t*)smem;
+    LDS_AS f32x4_t* red = (LDS_AS f32x4_t*)slot0;
 #pragma unroll
     for (int t = 0; t < TILES; t++)
 #pragma unroll
@@ -333,16 +307,21 @@ __device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, uint8_t
 
 template <int TILES, int MB>
 __device__ __forceinline__ void w4_decode(const t0_w4a16_params& p) {
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[W4DecCfg<TILES, MB>::SMEM];
+    using G = W4DecCfg<TILES, MB>;
+    // two distinct objects, so that the compiler tells the slots' DMAs apart
+    __shared__ __attribute__((aligned(1024))) uint8_t slot0[G::SLOT_BYTES];
+    __shared__ __attribute__((aligned(1024))) uint8_t slot1[G::SLOTS > 1 ? G::SLOT_BYTES : 1024];
     __shared__ uint32_t s_last;
+    LDS_AS uint8_t* s0 = (LDS_AS uint8_t*)slot0;
+    LDS_AS uint8_t* s1 = (LDS_AS uint8_t*)slot1;
     // zero points and scale type are uniform: one straight-line body each
     const bool zp = p.zeros != nullptr, sf32 = p.flags & T0_W4_SCALE_F32;
     if (zp) {
-        if (sf32) w4_decode_body<TILES, MB, true, true>(p, smem, &s_last);
-        else w4_decode_body<TILES, MB, true, false>(p, smem, &s_last);
+        if (sf32) w4_decode_body<TILES, MB, true, true>(p, s0, s1, &s_last);
+        else w4_decode_body<TILES, MB, true, false>(p, s0, s1, &s_last);
     } else {
-        if (sf32) w4_decode_body<TILES, MB, false, true>(p, smem, &s_last);
-        else w4_decode_body<TILES, MB, false, false>(p, smem, &s_last);
+        if (sf32) w4_decode_body<TILES, MB, false, true>(p, s0, s1, &s_last);
+        else w4_decode_body<TILES, MB, false, false>(p, s0, s1, &s_last);
     }
 }
 
