@@ -281,8 +281,12 @@ __device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, LDS_AS 
         const uint32_t slot = e * G::NT + tid;          // (t, mb, lane)
         v[e] = f32x4_t{0.f, 0.f, 0.f, 0.f};
         if (slot < (uint32_t)G::OUT_SLOTS) {
+            f32x4_t pw[G::WAVES];                        // every wave's partial in flight at once
 #pragma unroll
-            for (int q = 0; q < G::WAVES; q++) v[e] += red[q * G::OUT_SLOTS + slot];
+            for (int q = 0; q < G::WAVES; q++) pw[q] = red[q * G::OUT_SLOTS + slot];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int q = 0; q < G::WAVES; q++) v[e] += pw[q];   // in wave order
             if (sk > 1) st_agent_x4(rws, part * TILE_BYTES + slot * 16, v[e]);
         }
     }
