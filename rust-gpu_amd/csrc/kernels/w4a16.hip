@@ -75,7 +75,7 @@ T0_DEV void store_out4(const t0_w4a16_params& p, uint32_t m, uint32_t n, f32x4_t
 //        of column c0 + 16t + c holding k = 128g + 32h + [0, 32)
 //     S, Z -> the same slot by 4-byte DMAs: the group's scales of columns
 //        [c0, c1) and the zero-point words holding them
-//   Groups go in rounds of SLOTS (2 where LDS allows): every load of the
+//   Groups go in rounds of SLOTS (up to 4, as LDS and registers allow): every load of the
 //   round is issued, group by group, before the first group is consumed.
 //   Each group issues a fixed number of loads, so an explicit vmcnt wait
 //   lets a group's LDS data be read while the later groups' loads are still
@@ -123,17 +123,20 @@ struct W4DecCfg {
     // a wave's slot: A, then the group's scales (<= 256 B) and zero-point words (<= 64 B)
     static constexpr int S_OFF = GROUP_A, Z_OFF = GROUP_A + 256, WAVE_SLOT = GROUP_A + 512;
     static constexpr int SLOT_BYTES = WAVES * WAVE_SLOT;  // one group per wave
-    static constexpr int SLOTS = 2 * SLOT_BYTES <= 156 * 1024 ? 2 : 1;   // groups in flight per wave
+    // groups in flight per wave: as many as LDS holds, at most 2 under the
+    // 128-VGPR budget of 16 waves, else 4
+    static constexpr int SLOTS_LDS = 156 * 1024 / SLOT_BYTES;
+    static constexpr int SLOTS = SLOTS_LDS < (WAVES >= 16 ? 2 : 4) ? SLOTS_LDS : (WAVES >= 16 ? 2 : 4);
     static constexpr int OUT_SLOTS = TILES * MB * 64;     // 16-byte outputs per workgroup
     static constexpr int MAX_GROUP_LOADS = A_DMA + 2 + TILES;   // VMEM ops per group: A, S, Z, W
     static_assert(SLOTS * MAX_GROUP_LOADS < 64, "vmcnt range");
-    static_assert(SLOTS * SLOT_BYTES <= 156 * 1024, "LDS");
+    static_assert(SLOTS >= 1 && SLOTS * SLOT_BYTES <= 156 * 1024, "LDS");
     static_assert(WAVES * OUT_SLOTS * 16 <= SLOT_BYTES, "reduction fits slot 0");
     static_assert(TILES <= 4, "scale / zero-point DMA covers 64 columns");
 };
 
 template <int TILES, int MB, bool ZP, bool SF32>
-__device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, LDS_AS uint8_t* slot0, LDS_AS uint8_t* slot1,
+__device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, LDS_AS uint8_t* const (&slot)[4],
                                                uint32_t* s_last) {
     using G = W4DecCfg<TILES, MB>;
     typedef __attribute__((address_space(3))) void lds_void;
@@ -191,7 +194,7 @@ __device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, LDS_AS 
         for (int s = 0; s < G::SLOTS; s++) {
             const bool ok = j0 + s < nj;          // wave-uniform; a group past nj reads zeros and adds 0
             const uint32_t g = g_begin + wave + G::WAVES * (j0 + s);
-            LDS_AS uint8_t* dst = (s == 0 ? slot0 : slot1) + wave * G::WAVE_SLOT;
+            LDS_AS uint8_t* dst = slot[s] + wave * G::WAVE_SLOT;
 #pragma unroll
             for (int i = 0; i < G::A_DMA; i++)           // every block, so the count per group is fixed
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void*)(dst + i * 1024), 16,
@@ -214,8 +217,10 @@ __device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, LDS_AS 
 #pragma unroll
         for (int s = 0; s < G::SLOTS; s++) {
             if (s == 0) wait_vmcnt_fence<(G::SLOTS - 1) * GROUP_LOADS>();
+            else if (s == 1) wait_vmcnt_fence<(G::SLOTS - 2 > 0 ? G::SLOTS - 2 : 0) * GROUP_LOADS>();
+            else if (s == 2) wait_vmcnt_fence<(G::SLOTS - 3 > 0 ? G::SLOTS - 3 : 0) * GROUP_LOADS>();
             else wait_vmcnt_fence<0>();
-            const LDS_AS uint8_t* sp = (s == 0 ? slot0 : slot1) + wave * G::WAVE_SLOT;
+            const LDS_AS uint8_t* sp = slot[s] + wave * G::WAVE_SLOT;
             // activation fragments and sums of every row block, then one tile
             // at a time: unpack its weights once, use them for every row block
             bf16x8_t av[MB][4];
@@ -266,7 +271,7 @@ __device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, LDS_AS 
 
     // ---- sum the waves, in wave order ----------------------------------------
     __syncthreads();                                     // LDS free for the reduction
-    LDS_AS f32x4_t* red = (LDS_AS f32x4_t*)slot0;
+    LDS_AS f32x4_t* red = (LDS_AS f32x4_t*)slot[0];
 #pragma unroll
     for (int t = 0; t < TILES; t++)
 #pragma unroll
@@ -312,20 +317,22 @@ __device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, LDS_AS 
 template <int TILES, int MB>
 __device__ __forceinline__ void w4_decode(const t0_w4a16_params& p) {
     using G = W4DecCfg<TILES, MB>;
-    // two distinct objects, so that the compiler tells the slots' DMAs apart
+    // distinct objects, so that the compiler tells the slots' DMAs apart
     __shared__ __attribute__((aligned(1024))) uint8_t slot0[G::SLOT_BYTES];
-    __shared__ __attribute__((aligned(1024))) uint8_t slot1[G::SLOTS > 1 ? G::SLOT_BYTES : 1024];
+    __shared__ __attribute__((aligned(1024))) uint8_t slot1[G::SLOTS > 1 ? G::SLOT_BYTES : 16];
+    __shared__ __attribute__((aligned(1024))) uint8_t slot2[G::SLOTS > 2 ? G::SLOT_BYTES : 16];
+    __shared__ __attribute__((aligned(1024))) uint8_t slot3[G::SLOTS > 3 ? G::SLOT_BYTES : 16];
     __shared__ uint32_t s_last;
-    LDS_AS uint8_t* s0 = (LDS_AS uint8_t*)slot0;
-    LDS_AS uint8_t* s1 = (LDS_AS uint8_t*)slot1;
+    LDS_AS uint8_t* const sl[4] = {(LDS_AS uint8_t*)slot0, (LDS_AS uint8_t*)slot1, (LDS_AS uint8_t*)slot2,
+                                   (LDS_AS uint8_t*)slot3};
     // zero points and scale type are uniform: one straight-line body each
     const bool zp = p.zeros != nullptr, sf32 = p.flags & T0_W4_SCALE_F32;
     if (zp) {
-        if (sf32) w4_decode_body<TILES, MB, true, true>(p, s0, s1, &s_last);
-        else w4_decode_body<TILES, MB, true, false>(p, s0, s1, &s_last);
+        if (sf32) w4_decode_body<TILES, MB, true, true>(p, sl, &s_last);
+        else w4_decode_body<TILES, MB, true, false>(p, sl, &s_last);
     } else {
-        if (sf32) w4_decode_body<TILES, MB, false, true>(p, s0, s1, &s_last);
-        else w4_decode_body<TILES, MB, false, false>(p, s0, s1, &s_last);
+        if (sf32) w4_decode_body<TILES, MB, false, true>(p, sl, &s_last);
+        else w4_decode_body<TILES, MB, false, false>(p, sl, &s_last);
     }
 }
 

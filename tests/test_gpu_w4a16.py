@@ -147,6 +147,34 @@ def test_w4a16_decode_headline(rt, dev):
     assert np.array_equal(got_i.astype(np.int64), want)
 
 
+@pytest.mark.parametrize("m", [3, 16])
+def test_w4a16_decode_wide_n_zero_points(rt, dev, m):
+    """N = 14336 gives 56 columns per workgroup: the 4-tile decode instance
+    (8 waves, four groups in flight per wave), with per-group zero points;
+    integer activations and unit scales make every output an exact integer."""
+    rng = np.random.default_rng(45 + m)
+    n, k, gs = 14336, 4096, 128
+    qw, s, zw = make_w4(rng, n, k, gs, per_group_zeros=True)
+    plan, _ = rt.w4a16_plan(0, 0, 0, 0, 0, m, n, k, group_size=gs)
+    assert plan.startswith("t0k_w4a16_decode_t4_mb1"), plan
+    ones = np.full_like(s, 0x3F80)
+    ai = rng.integers(-3, 4, size=(m, k))
+    got = run_w4(rt, dev, bf16(ai), qw, ones, zw, m, n, k, gs, out_f32=True)
+    q = orc.int4_unpack(qw.view(np.uint8), n * k).reshape(n, k).astype(np.int64)
+    z = np.zeros((k // gs, n), np.int64)
+    for j in range(8):
+        z[:, j::8] = ((zw >> np.uint32(4 * j)) & 0xF).astype(np.int64)
+    w = q - np.repeat(z.T, gs, axis=1)                    # [n][k]
+    assert np.array_equal(got.astype(np.int64), ai.astype(np.int64) @ w.T)
+    # random activations and scales on a column block, against the oracle
+    a = bf16(rng.standard_normal((m, k)))
+    got = run_w4(rt, dev, a, qw, s, zw, m, n, k, gs)
+    j0, j1 = 8192, 8192 + 1024
+    ref = orc.w4a16(a, qw[j0:j1].copy(), s[:, j0:j1].copy(), zw[:, j0 // 8:j1 // 8].copy(), 0, m, j1 - j0, k, gs)
+    check_close(got[:, j0:j1], ref, w4_tol(a, qw[j0:j1].copy(), s[:, j0:j1].copy(), zw[:, j0 // 8:j1 // 8].copy(),
+                                           0, j1 - j0, k, gs), f"decode wide m={m}")
+
+
 @pytest.mark.parametrize("m,n", [(256, 512), (300, 264), (1024, 256)])
 def test_w4a16_prefill(rt, dev, m, n):
     rng = np.random.default_rng(m + n)
