@@ -388,6 +388,41 @@ int t0_bf16_matmul_backward_weight(t0_runtime* rt, uint64_t x, uint64_t dy, uint
 int t0_bf16_matmul_with_wt_bf16(t0_runtime* rt, uint64_t x, uint64_t wt, uint64_t y, uint32_t m, uint32_t k,
                                 uint32_t n);
 
+/* ------------------------------------------- residual add + RMSNorm ---- */
+/* x2 = residual (+ hidden); inv_rms = 1 / sqrt(sum(x2^2)/d + eps);
+ * normed = x2 * inv_rms * gamma.  f32 device buffers, dense rows.          */
+
+/* Replaces the reference kernel build_ffn_fused_rmsnorm_gemm and its CPU form
+ * (src/t0/ffn_fused_kernels.rs:54-237): output[r] = sum_i normed[r,i] *
+ * weight[r*d + i] for rows r < m.  The code object also exports the kernel
+ * itself as "ffn_fused_rmsnorm_gemm" (128-lane workgroups, one per row, the
+ * reference's 48-byte kernargs) for raw t0_kernel_load + t0_dispatch. */
+int t0_ffn_fused_rmsnorm_gemm(t0_runtime* rt, uint64_t residual, uint64_t hidden, uint64_t gamma, uint64_t weight,
+                              uint64_t output, uint32_t m, uint32_t d, float eps);
+/* Residual add + RMSNorm over rows (src/t0/rmsnorm_kernels.rs:140-153 on the
+ * residual sum of ffn_fused_kernels.rs:215-224): out[r][0..d) = normed as
+ * bf16 (RNE, out_bf16 != 0) or f32, zeros in [d, ld_out) (0 = d); x2_out
+ * (may be 0) receives x2.  hidden may be 0. */
+int t0_rmsnorm(t0_runtime* rt, uint64_t residual, uint64_t hidden, uint64_t gamma, uint64_t out, uint64_t x2_out,
+               uint32_t rows, uint32_t d, uint32_t ld_out, float eps, int out_bf16);
+typedef struct t0_rmsnorm_desc {
+    uint64_t residual, hidden, gamma;  /* f32 [m][k], [m][k] or 0, [k] */
+    uint64_t x2_out;                   /* f32 [m][k] or 0 */
+    float eps;
+    uint32_t pad_;
+} t0_rmsnorm_desc;
+/* fused_rmsnorm_gemm / fused_residual_rmsnorm_gemm
+ * (src/ignis/ops/fused_rmsnorm_gemm.rs:33-154) on an INT4 weight:
+ * C[m,n] = normed[m,:] . W^T with W as in t0_w4a16_desc (d->a and d->lda are
+ * ignored).  m == 1: one decode kernel with the residual add and RMSNorm in
+ * front (the per-row 1/rms is applied after the k sum); other m: t0_rmsnorm
+ * to bf16 in the runtime's staging buffer, then t0_w4a16_gemm. */
+int t0_rmsnorm_w4a16(t0_runtime* rt, const t0_w4a16_desc* d, const t0_rmsnorm_desc* nd);
+/* The same with a dense f32 weight W[k,n] (the Ignis prefill path:
+ * rmsnorm, then bf16_matmul): Y[m,n] = bf16(normed) . bf16(W), f32 out. */
+int t0_rmsnorm_matmul(t0_runtime* rt, uint64_t residual, uint64_t hidden, uint64_t gamma, uint64_t w, uint64_t y,
+                      uint64_t x2_out, uint32_t m, uint32_t k, uint32_t n, float eps);
+
 #ifdef __cplusplus
 }
 #endif

@@ -285,3 +285,65 @@ void orc_w4a16_dequant(const uint32_t* qw, const uint16_t* scales,
         for (size_t kk = 0; kk < k; kk++)
             w[j * k + kk] = w4_weight(qw, scales, zeros, zc, j, kk, n, k, gs);
 }
+
+/* ------------------------------------------------------------------------ */
+/* Decode neighbours: residual add + RMSNorm (+ projection)                 */
+/* ------------------------------------------------------------------------ */
+
+/* x2 = residual + hidden (hidden may be NULL: x2 = residual);
+ * inv_rms = 1 / sqrt(sum(x2^2) / d + eps), the square sum taken in order;
+ * normed[i] = x2[i] * inv_rms * gamma[i], multiplied left to right.
+ * Ref: src/t0/rmsnorm_kernels.rs:140-153 (cpu_rmsnorm_forward) on the
+ *      residual sum of src/t0/ffn_fused_kernels.rs:215-224.
+ * x2_out and inv_rms_out may be NULL. */
+void orc_rmsnorm_rows(const float* res, const float* hid, const float* gamma,
+                      float* normed, float* x2_out, float* inv_rms_out,
+                      size_t m, size_t d, float eps)
+{
+    for (size_t r = 0; r < m; r++) {
+        float sum_sq = 0.0f;
+        for (size_t i = 0; i < d; i++) {
+            float x2 = hid ? res[r * d + i] + hid[r * d + i] : res[r * d + i];
+            if (x2_out) x2_out[r * d + i] = x2;
+            float sq = x2 * x2;
+            sum_sq = sum_sq + sq;
+        }
+        float mean_sq = sum_sq / (float)d;
+        float inv_rms = 1.0f / sqrtf(mean_sq + eps);
+        if (inv_rms_out) inv_rms_out[r] = inv_rms;
+        for (size_t i = 0; i < d; i++) {
+            float x2 = hid ? res[r * d + i] + hid[r * d + i] : res[r * d + i];
+            float t = x2 * inv_rms;
+            normed[r * d + i] = t * gamma[i];
+        }
+    }
+}
+
+/* The reference's fused residual add + RMSNorm + per-row projection:
+ *   out[row] = sum_i (x2[row,i] * inv_rms_row * gamma[i]) * weight[row*d + i]
+ * with the products and the running sum in f32, in order, no FMA.
+ * Ref: src/t0/ffn_fused_kernels.rs:203-237 (cpu_ffn_fused_rmsnorm_gemm),
+ *      the GPU kernel's semantics at :54-189. */
+void orc_ffn_fused_rmsnorm_gemm(const float* res, const float* hid, const float* gamma,
+                                const float* weight, float* out, size_t m, size_t d, float eps)
+{
+    for (size_t r = 0; r < m; r++) {
+        float sum_sq = 0.0f;
+        for (size_t i = 0; i < d; i++) {
+            float x2 = res[r * d + i] + hid[r * d + i];
+            float sq = x2 * x2;
+            sum_sq = sum_sq + sq;
+        }
+        float mean_sq = sum_sq / (float)d;
+        float inv_rms = 1.0f / sqrtf(mean_sq + eps);
+        float acc = 0.0f;
+        for (size_t i = 0; i < d; i++) {
+            float x2 = res[r * d + i] + hid[r * d + i];
+            float t = x2 * inv_rms;
+            float normed = t * gamma[i];
+            float p = normed * weight[r * d + i];
+            acc = acc + p;
+        }
+        out[r] = acc;
+    }
+}

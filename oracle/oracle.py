@@ -69,6 +69,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_w4a16_rows.argtypes = [_P, _P, _P, _P, ctypes.c_uint32, _P, _SZ, _SZ, _SZ, _SZ, _SZ]
     L.orc_w4a16.argtypes = [_P, _P, _P, _P, ctypes.c_uint32, _P, _SZ, _SZ, _SZ, _SZ]
     L.orc_w4a16_dequant.argtypes = [_P, _P, _P, ctypes.c_uint32, _P, _SZ, _SZ, _SZ]
+    L.orc_rmsnorm_rows.argtypes = [_P, _P, _P, _P, _P, _P, _SZ, _SZ, ctypes.c_float]
+    L.orc_ffn_fused_rmsnorm_gemm.argtypes = [_P, _P, _P, _P, _P, _SZ, _SZ, ctypes.c_float]
 
 
 def _ptr(a: np.ndarray | None):
@@ -296,3 +298,32 @@ def gptq_from_bytes(raw: bytes):
     scales = np.frombuffer(raw, dtype="<f4", count=n_params, offset=12 + packed_len)
     zps = np.frombuffer(raw, dtype="<i4", count=n_params, offset=12 + packed_len + 4 * n_params)
     return rows, cols, gs, n_groups, packed, scales, zps
+
+
+# ------------------------------------------------------- decode neighbours --
+
+def rmsnorm_rows(res: np.ndarray, hid: np.ndarray | None, gamma: np.ndarray, eps: float):
+    """(normed, x2, inv_rms) of residual add + RMSNorm, f32 in order.
+    Ref: src/t0/rmsnorm_kernels.rs:140-153 on src/t0/ffn_fused_kernels.rs:215-224."""
+    res = np.ascontiguousarray(res, dtype=np.float32)
+    m, d = res.shape
+    h = None if hid is None else np.ascontiguousarray(hid, dtype=np.float32)
+    g = np.ascontiguousarray(gamma, dtype=np.float32).reshape(d)
+    normed = np.empty((m, d), np.float32)
+    x2 = np.empty((m, d), np.float32)
+    inv = np.empty(m, np.float32)
+    lib().orc_rmsnorm_rows(_ptr(res), _ptr(h), _ptr(g), _ptr(normed), _ptr(x2), _ptr(inv), m, d, eps)
+    return normed, x2, inv
+
+
+def ffn_fused_rmsnorm_gemm(res, hid, gamma, weight, eps: float) -> np.ndarray:
+    """out[row] = sum_i (x2[row,i] * inv_rms * gamma[i]) * weight[row,i].
+    Ref: src/t0/ffn_fused_kernels.rs:203-237."""
+    res = np.ascontiguousarray(res, dtype=np.float32)
+    m, d = res.shape
+    hid = np.ascontiguousarray(hid, dtype=np.float32)
+    g = np.ascontiguousarray(gamma, dtype=np.float32).reshape(d)
+    w = np.ascontiguousarray(weight, dtype=np.float32).reshape(m, d)
+    out = np.empty(m, np.float32)
+    lib().orc_ffn_fused_rmsnorm_gemm(_ptr(res), _ptr(hid), _ptr(g), _ptr(w), _ptr(out), m, d, eps)
+    return out

@@ -1352,3 +1352,127 @@ int t0_bf16_matmul_with_wt_bf16(t0_runtime* rt, uint64_t x, uint64_t wt, uint64_
 }
 
 }  // extern "C"
+
+// ------------------------------------------------- decode neighbours ----
+// Residual add + RMSNorm in front of the projections: the reference's fused
+// kernel (src/t0/ffn_fused_kernels.rs), the Ignis ops built on it
+// (src/ignis/ops/fused_rmsnorm_gemm.rs) with an INT4 or a dense weight.
+namespace {
+
+bool aligned8(uint64_t p) { return (p & 7) == 0; }
+
+int launch_rmsnorm(t0_runtime* rt, uint64_t res, uint64_t hid, uint64_t gamma, uint64_t out, uint64_t x2_out,
+                   uint32_t rows, uint32_t d, uint32_t ld_out, float eps, bool out_bf16) {
+    hipFunction_t f;
+    int r = get_fn(rt, "t0k_rmsnorm", &f);
+    if (r) return r;
+    t0_rmsnorm_params p;
+    memset(&p, 0, sizeof p);
+    p.res = (const float*)res; p.hid = (const float*)hid; p.gamma = (const float*)gamma;
+    p.out = (void*)out; p.x2_out = (float*)x2_out;
+    p.rows = rows; p.d = d; p.ld_out = ld_out; p.out_bf16 = out_bf16; p.eps = eps;
+    return launch(rt, f, rows, 1, 1, 256, p);
+}
+
+}  // namespace
+
+extern "C" {
+
+int t0_ffn_fused_rmsnorm_gemm(t0_runtime* rt, uint64_t residual, uint64_t hidden, uint64_t gamma, uint64_t weight,
+                              uint64_t output, uint32_t m, uint32_t d, float eps) {
+    if (!rt || !residual || !hidden || !gamma || !weight || !output) return fail(T0_ERR_INVALID, "null argument");
+    if (!m || !d) return fail(T0_ERR_INVALID, "empty problem m=%u d=%u", m, d);
+    int r = set_dev(rt);
+    if (r) return r;
+    hipFunction_t f;
+    r = get_fn(rt, "ffn_fused_rmsnorm_gemm", &f);
+    if (r) return r;
+    t0_ffn_params p;
+    p.residual = (const float*)residual; p.hidden = (const float*)hidden; p.gamma = (const float*)gamma;
+    p.weight = (const float*)weight; p.output = (float*)output; p.D = d; p.eps = eps;
+    return launch(rt, f, m, 1, 1, 128, p);
+}
+
+int t0_rmsnorm(t0_runtime* rt, uint64_t residual, uint64_t hidden, uint64_t gamma, uint64_t out, uint64_t x2_out,
+               uint32_t rows, uint32_t d, uint32_t ld_out, float eps, int out_bf16) {
+    if (!rt || !residual || !gamma || !out) return fail(T0_ERR_INVALID, "null argument");
+    if (!rows || !d) return fail(T0_ERR_INVALID, "empty problem rows=%u d=%u", rows, d);
+    if (ld_out == 0) ld_out = d;
+    if (ld_out < d) return fail(T0_ERR_INVALID, "ld_out %u < d %u", ld_out, d);
+    int r = set_dev(rt);
+    if (r) return r;
+    return launch_rmsnorm(rt, residual, hidden, gamma, out, x2_out, rows, d, ld_out, eps, out_bf16 != 0);
+}
+
+int t0_rmsnorm_w4a16(t0_runtime* rt, const t0_w4a16_desc* d, const t0_rmsnorm_desc* nd) {
+    if (!rt || !d || !nd || !nd->residual || !nd->gamma || !d->qweight || !d->scales || !d->c)
+        return fail(T0_ERR_INVALID, "null argument");
+    if (!d->m || !d->k) return fail(T0_ERR_INVALID, "empty problem");
+    int r = set_dev(rt);
+    if (r) return r;
+    const bool vec_ok = aligned8(nd->residual) && aligned8(nd->hidden) && aligned8(nd->gamma) && aligned8(nd->x2_out);
+    if (d->m == 1 && vec_ok) {
+        t0_w4a16_desc d1 = *d;
+        d1.a = 0; d1.lda = 0; d1.split_k = 1;        // one partition: every workgroup sees the whole row
+        W4Plan pl;
+        r = w4_plan(rt, &d1, pl);
+        if (r) return r;
+        if (pl.kind == 1) {
+            if (!d->zeros && d->zero_const > 15) return fail(T0_ERR_INVALID, "zero_const must be 0..15");
+            const uint32_t tiles = pl.bn / 16;
+            char sym[64];
+            snprintf(sym, sizeof sym, "t0k_w4a16_decode_norm_t%u", tiles);
+            hipFunction_t f;
+            r = get_fn(rt, sym, &f);
+            if (r) return r;
+            t0_w4a16_params p;
+            memset(&p, 0, sizeof p);
+            p.qweight = (const uint32_t*)d->qweight;
+            p.scales = (const void*)d->scales;
+            p.zeros = (const uint32_t*)d->zeros;
+            p.C = (void*)d->c;
+            p.M = 1; p.N = d->n; p.K = d->k;
+            p.lda = d->k;
+            p.ldc = d->ldc ? d->ldc : d->n;
+            p.group_size = d->group_size;
+            p.zero_const = d->zero_const;
+            p.flags = (d->scales_f32 ? T0_W4_SCALE_F32 : 0) | (d->out_f32 ? T0_W4_OUT_F32 : 0);
+            p.split_k = 1;
+            p.norm_res = (const float*)nd->residual;
+            p.norm_hid = (const float*)nd->hidden;
+            p.norm_gamma = (const float*)nd->gamma;
+            p.norm_x2 = (float*)nd->x2_out;
+            p.norm_eps = nd->eps;
+            return launch(rt, f, pl.gx, 1, 1, 64 * t0_w4_decode_norm_waves((int)tiles), p);
+        }
+    }
+    // any other shape: normalised bf16 activations into the staging buffer,
+    // then the W4A16 GEMM on them
+    const size_t a_bytes = align256((size_t)d->m * d->k * 2);
+    r = ensure_stage(rt, a_bytes);
+    if (r) return r;
+    const uint64_t sa = (uint64_t)rt->stage;
+    r = launch_rmsnorm(rt, nd->residual, nd->hidden, nd->gamma, sa, nd->x2_out, d->m, d->k, d->k, nd->eps, true);
+    if (r) return r;
+    t0_w4a16_desc d2 = *d;
+    d2.a = sa;
+    d2.lda = d->k;
+    return t0_w4a16_gemm(rt, &d2);
+}
+
+int t0_rmsnorm_matmul(t0_runtime* rt, uint64_t residual, uint64_t hidden, uint64_t gamma, uint64_t w, uint64_t y,
+                      uint64_t x2_out, uint32_t m, uint32_t k, uint32_t n, float eps) {
+    int r = matmul_args(rt, residual, w, y, m, k, n);
+    if (r) return r;
+    if (!gamma) return fail(T0_ERR_INVALID, "null gamma");
+    const uint32_t k8 = round8(k), n8 = round8(n);
+    const size_t a_bytes = align256((size_t)m * k8 * 2), b_bytes = align256((size_t)k8 * n8 * 2);
+    r = ensure_stage(rt, a_bytes + b_bytes);
+    if (r) return r;
+    const uint64_t sa = (uint64_t)rt->stage, sb = sa + a_bytes;
+    if ((r = launch_rmsnorm(rt, residual, hidden, gamma, sa, x2_out, m, k, k8, eps, true))) return r;   // -> [m][k8]
+    if ((r = stage_cvt(rt, w, n, k, n, sb, n8, k8))) return r;                                         // W -> [k8][n8]
+    return staged_gemm(rt, sa, k8, sb, n8, y, n, m, n, k8, true);
+}
+
+}  // extern "C"

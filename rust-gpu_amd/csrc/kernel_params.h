@@ -68,7 +68,43 @@ typedef struct t0_w4a16_params {
     uint32_t flags;
     uint32_t split_k;         // decode: K partitions (>= 1)
     uint32_t pad_;
+    // fused residual add + RMSNorm in front of the decode (t0k_w4a16_decode_norm_*,
+    // M == 1): the activations are x2 * inv_rms * gamma with x2 = res (+ hid)
+    const float* norm_res;    // [K]
+    const float* norm_hid;    // [K] or NULL
+    const float* norm_gamma;  // [K]
+    float* norm_x2;           // [K] or NULL: x2, written by workgroup 0
+    float norm_eps;
+    uint32_t pad2_;
 } t0_w4a16_params;
+
+// The reference's fused residual add + RMSNorm + row projection kernel,
+// byte for byte its kernarg layout (src/t0/ffn_fused_kernels.rs:47-49):
+// [residual, hidden, gamma, weight, output: u64; D: u32; eps: f32].
+typedef struct t0_ffn_params {
+    const float* residual;
+    const float* hidden;
+    const float* gamma;
+    const float* weight;
+    float* output;
+    uint32_t D;
+    float eps;
+} t0_ffn_params;
+
+// Residual add + RMSNorm over rows: out = x2 * inv_rms * gamma (bf16 RNE or
+// f32), x2 = res (+ hid), optionally written back.
+typedef struct t0_rmsnorm_params {
+    const float* res;
+    const float* hid;         // or NULL
+    const float* gamma;
+    void* out;
+    float* x2_out;            // or NULL
+    uint32_t rows, d;
+    uint32_t ld_out;          // elements
+    uint32_t out_bf16;
+    float eps;
+    uint32_t pad_;
+} t0_rmsnorm_params;
 
 // Reference dequant kernel arguments (src/t0/quant_kernels.rs:45-47):
 // [packed_weights, scales(f32), zero_points(i32), output; rows, cols]
@@ -105,4 +141,7 @@ typedef struct t0_aux_params {
 constexpr int t0_w4_decode_waves(int tiles, int mb) {
     return (tiles * mb <= 3 && 32 / mb >= 16) ? 16 : (tiles * mb <= 8 ? 8 : 4);
 }
+// The same for t0k_w4a16_decode_norm_t<tiles> (M == 1 with the fused RMSNorm,
+// whose residual / hidden / gamma registers leave 16 waves room for 2 tiles).
+constexpr int t0_w4_decode_norm_waves(int tiles) { return tiles <= 2 ? 16 : 8; }
 #endif

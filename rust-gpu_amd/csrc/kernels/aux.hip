@@ -140,6 +140,79 @@ __device__ __forceinline__ void cvt_t_bf16(const t0_aux_params& p) {
     }
 }
 
+// Sum of v over the NW waves of the workgroup, the same value in every lane:
+// a butterfly within each wave, then the wave totals in wave order (so the
+// result does not depend on timing).  sh holds NW floats; the caller
+// separates two uses of the same sh with a barrier.
+template <int NW>
+T0_DEV float block_sum(float v, float* sh) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = sh[0];
+#pragma unroll
+    for (int w = 1; w < NW; w++) t += sh[w];
+    return t;
+}
+
+// The reference's fused residual add + RMSNorm + row projection
+// (src/t0/ffn_fused_kernels.rs:54-189; CPU form :203-237), one 128-lane
+// workgroup per row r:
+//   x2 = residual[r] + hidden[r];  inv_rms = 1 / sqrt(sum(x2^2) / D + eps)
+//   output[r] = sum_i (x2[i] * inv_rms * gamma[i]) * weight[r*D + i]
+// Two passes over the row, the second re-reading x2 (L2-resident), as the
+// reference kernel does.
+__device__ __forceinline__ void ffn_fused_rmsnorm_gemm(const t0_ffn_params& p) {
+    __shared__ float sh[2][2];
+    const uint32_t D = p.D, t = threadIdx.x;
+    const size_t base = (size_t)blockIdx.x * D;
+    float ssq = 0.0f;
+    for (uint32_t i = t; i < D; i += 128) {
+        const float x2 = p.residual[base + i] + p.hidden[base + i];
+        ssq += x2 * x2;
+    }
+    ssq = block_sum<2>(ssq, sh[0]);
+    const float inv_rms = 1.0f / sqrtf(ssq / (float)D + p.eps);
+    float acc = 0.0f;
+    for (uint32_t i = t; i < D; i += 128) {
+        const float x2 = p.residual[base + i] + p.hidden[base + i];
+        acc += ((x2 * inv_rms) * p.gamma[i]) * p.weight[base + i];
+    }
+    acc = block_sum<2>(acc, sh[1]);
+    if (t == 0) p.output[blockIdx.x] = acc;
+}
+
+// Residual add + RMSNorm over rows (src/t0/rmsnorm_kernels.rs:140-153 on the
+// residual sum of ffn_fused_kernels.rs:215-224), one 256-lane workgroup per
+// row: out[r][i] = x2 * inv_rms * gamma[i] as bf16 (RNE) or f32, zeros in
+// columns [d, ld_out), and x2 written back to x2_out when given (the updated
+// residual stream).
+__device__ __forceinline__ void rmsnorm_rows(const t0_rmsnorm_params& p) {
+    __shared__ float sh[4];
+    const uint32_t d = p.d, t = threadIdx.x, r = blockIdx.x;
+    const size_t base = (size_t)r * d;
+    float ssq = 0.0f;
+    for (uint32_t i = t; i < d; i += 256) {
+        const float x2 = p.hid ? p.res[base + i] + p.hid[base + i] : p.res[base + i];
+        if (p.x2_out) p.x2_out[base + i] = x2;
+        ssq += x2 * x2;
+    }
+    ssq = block_sum<4>(ssq, sh);
+    const float inv_rms = 1.0f / sqrtf(ssq / (float)d + p.eps);
+    const size_t ob = (size_t)r * p.ld_out;
+    for (uint32_t i = t; i < d; i += 256) {
+        const float x2 = p.hid ? p.res[base + i] + p.hid[base + i] : p.res[base + i];
+        const float y = (x2 * inv_rms) * p.gamma[i];
+        if (p.out_bf16) ((uint16_t*)p.out)[ob + i] = (uint16_t)(pack2_bf16_rne(y, 0.f) & 0xFFFFu);
+        else ((float*)p.out)[ob + i] = y;
+    }
+    for (uint32_t i = d + t; i < p.ld_out; i += 256) {   // a padded row: zeros after the data
+        if (p.out_bf16) ((uint16_t*)p.out)[ob + i] = 0;
+        else ((float*)p.out)[ob + i] = 0.0f;
+    }
+}
+
 // out[m][n] = padded[m][n_pad]  (src/t0/math.rs t0_unpad_2d semantics).
 __device__ __forceinline__ void unpad_2d(const t0_aux_params& p) {
     const uint64_t e = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -157,6 +230,12 @@ extern "C" __global__ void __launch_bounds__(256) t0k_f32_to_bf16(const t0_aux_p
 extern "C" __global__ void __launch_bounds__(256) t0_unpad_2d(const t0_aux_params p) { t0::unpad_2d(p); }
 extern "C" __global__ void __launch_bounds__(256) t0k_cvt_pad_bf16(const t0_aux_params p) { t0::cvt_pad_bf16(p); }
 extern "C" __global__ void __launch_bounds__(256) t0k_cvt_t_bf16(const t0_aux_params p) { t0::cvt_t_bf16(p); }
+// The reference kernel's name, 128-lane workgroups and 48-byte kernargs, so
+// its raw dispatch (grid = M*128 work-items) works unchanged.
+extern "C" __global__ void __launch_bounds__(128) ffn_fused_rmsnorm_gemm(const t0_ffn_params p) {
+    t0::ffn_fused_rmsnorm_gemm(p);
+}
+extern "C" __global__ void __launch_bounds__(256) t0k_rmsnorm(const t0_rmsnorm_params p) { t0::rmsnorm_rows(p); }
 
 // Plain 16-byte-per-lane copy of n16 chunks: the calibration kernel whose
 // known byte count scales the FETCH_SIZE / WRITE_SIZE counters.

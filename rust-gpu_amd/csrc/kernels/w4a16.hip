@@ -114,10 +114,11 @@ T0_DEV bf16x8_t unpack8_128(uint32_t w, uint32_t bits4300) {
     return __builtin_bit_cast(bf16x8_t, r);
 }
 
-template <int TILES, int MB>
+template <int TILES, int MB, bool NORM = false>
 struct W4DecCfg {
     // as many waves as the per-group registers allow (16 waves: <= 128 VGPRs)
-    static constexpr int WAVES = t0_w4_decode_waves(TILES, MB), NT = 64 * WAVES;
+    static constexpr int WAVES = NORM ? t0_w4_decode_norm_waves(TILES) : t0_w4_decode_waves(TILES, MB);
+    static constexpr int NT = 64 * WAVES;
     static constexpr int GROUP_A = 16 * MB * 256;         // A bytes of one group
     static constexpr int A_DMA = GROUP_A / 1024;          // 4-row DMA blocks per group
     // a wave's slot: A, then the group's scales (<= 256 B) and zero-point words (<= 64 B)
@@ -133,12 +134,14 @@ struct W4DecCfg {
     static_assert(SLOTS >= 1 && SLOTS * SLOT_BYTES <= 156 * 1024, "LDS");
     static_assert(WAVES * OUT_SLOTS * 16 <= SLOT_BYTES, "reduction fits slot 0");
     static_assert(TILES <= 4, "scale / zero-point DMA covers 64 columns");
+    static_assert(WAVES * OUT_SLOTS * 16 + WAVES * 4 <= SLOT_BYTES, "wave sums of squares after the partials");
 };
 
-template <int TILES, int MB, bool ZP, bool SF32>
+template <int TILES, int MB, bool ZP, bool SF32, bool NORM>
 __device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, LDS_AS uint8_t* const (&slot)[4],
                                                uint32_t* s_last) {
-    using G = W4DecCfg<TILES, MB>;
+    using G = W4DecCfg<TILES, MB, NORM>;
+    static_assert(!NORM || MB == 1, "the fused RMSNorm decode takes one activation row");
     typedef __attribute__((address_space(3))) void lds_void;
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -151,7 +154,8 @@ __device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, LDS_AS 
     const uint32_t g_begin = part * GP;
     const uint32_t c = lane & 15, h = lane >> 4;
     constexpr uint32_t ES = SF32 ? 4 : 2;               // scale bytes
-    constexpr int GROUP_LOADS = G::A_DMA + 1 + (ZP ? 1 : 0) + TILES;   // VMEM ops per group: A, S, Z, W
+    // VMEM ops per group: A (DMA blocks, or residual / hidden / gamma pairs), S, Z, W
+    constexpr int GROUP_LOADS = (NORM ? 3 : G::A_DMA) + 1 + (ZP ? 1 : 0) + TILES;
 
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A);
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.scales);
@@ -175,6 +179,20 @@ __device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, LDS_AS 
     const uint32_t zb = c0 / 8;
     const uint32_t s_lane = (SF32 ? c0 + lane : c0 + 2 * lane) < c1 ? (SF32 ? c0 + lane : c0 + 2 * lane) * ES : OOB_OFFSET;
     const uint32_t z_lane = (ZP && lane < 9 && (zb + lane) * 8 < c1) ? (zb + lane) * 4 : OOB_OFFSET;
+    // fused RMSNorm: lane l owns k = 128g + 2l, 2l+1 of each group; rows 1..15
+    // of the activation slots stay zero, row 0 is written per group
+    const __amdgpu_buffer_rsrc_t rn_res = make_rsrc(p.norm_res), rn_hid = make_rsrc(p.norm_hid);
+    const __amdgpu_buffer_rsrc_t rn_gam = make_rsrc(p.norm_gamma);
+    const uint32_t hid_ok = p.norm_hid != nullptr;
+    const bool store_x2 = NORM && p.norm_x2 != nullptr && wg == 0 && part == 0;
+    float ssq = 0.0f;                                   // this lane's share of sum(x2^2)
+    if constexpr (NORM) {
+#pragma unroll
+        for (int s = 0; s < G::SLOTS; s++)
+#pragma unroll
+            for (int q = 0; q < G::GROUP_A / 1024; q++)
+                *(LDS_AS u32x4_t*)(slot[s] + wave * G::WAVE_SLOT + q * 1024 + lane * 16) = u32x4_t{0u, 0u, 0u, 0u};
+    }
     const float zc_const = 128.0f + (float)p.zero_const;
     const uint32_t bits4300 = __builtin_amdgcn_mov_dpp(0x43004300u, 0xE4, 0xF, 0xF, false);  // in a VGPR
     const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, u32x4_t{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
@@ -190,16 +208,24 @@ __device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, LDS_AS 
     for (uint32_t j0 = 0; j0 < nj; j0 += G::SLOTS) {
         // ---- 1. every load of the round, group by group ----------------------
         u32x4_t wq[G::SLOTS][TILES];
+        u32x2_t nr[G::SLOTS], nh[G::SLOTS], ng[G::SLOTS];   // NORM: residual, hidden, gamma pairs
 #pragma unroll
         for (int s = 0; s < G::SLOTS; s++) {
             const bool ok = j0 + s < nj;          // wave-uniform; a group past nj reads zeros and adds 0
             const uint32_t g = g_begin + wave + G::WAVES * (j0 + s);
             LDS_AS uint8_t* dst = slot[s] + wave * G::WAVE_SLOT;
+            if constexpr (NORM) {
+                const uint32_t ko = ok ? (g * 128 + 2 * lane) * 4 : OOB_OFFSET;
+                nr[s] = buffer_load_x2(rn_res, ko);
+                nh[s] = buffer_load_x2(rn_hid, hid_ok ? ko : OOB_OFFSET);
+                ng[s] = buffer_load_x2(rn_gam, ko);
+            } else {
 #pragma unroll
-            for (int i = 0; i < G::A_DMA; i++)           // every block, so the count per group is fixed
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void*)(dst + i * 1024), 16,
-                                                        ok && a_off[i] != OOB_OFFSET ? a_off[i] + g * 256 : OOB_OFFSET,
-                                                        0, 0, 0);
+                for (int i = 0; i < G::A_DMA; i++)       // every block, so the count per group is fixed
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void*)(dst + i * 1024), 16,
+                                                            ok && a_off[i] != OOB_OFFSET ? a_off[i] + g * 256 : OOB_OFFSET,
+                                                            0, 0, 0);
+            }
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(dst + G::S_OFF), 4,
                                                     ok && s_lane != OOB_OFFSET ? s_lane + g * N * ES : OOB_OFFSET, 0, 0, 0);
             if (ZP)
@@ -221,6 +247,20 @@ __device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, LDS_AS 
             else if (s == 2) wait_vmcnt_fence<(G::SLOTS - 3 > 0 ? G::SLOTS - 3 : 0) * GROUP_LOADS>();
             else wait_vmcnt_fence<0>();
             const LDS_AS uint8_t* sp = slot[s] + wave * G::WAVE_SLOT;
+            if constexpr (NORM) {
+                // x2 = res + hid; row 0 of the slot = bf16(x2 * gamma); the
+                // per-row 1/rms is a common factor applied after the sum
+                const float x0 = __uint_as_float(nr[s][0]) + __uint_as_float(nh[s][0]);
+                const float x1 = __uint_as_float(nr[s][1]) + __uint_as_float(nh[s][1]);
+                ssq += x0 * x0;
+                ssq += x1 * x1;
+                if (store_x2 && j0 + s < nj) {
+                    const uint32_t g = g_begin + wave + G::WAVES * (j0 + s);
+                    *(u32x2_t*)(p.norm_x2 + g * 128 + 2 * lane) = u32x2_t{__float_as_uint(x0), __float_as_uint(x1)};
+                }
+                *(LDS_AS uint32_t*)(slot[s] + wave * G::WAVE_SLOT + lane * 4) =
+                    pack2_bf16_rne(x0 * __uint_as_float(ng[s][0]), x1 * __uint_as_float(ng[s][1]));
+            }
             // activation fragments and sums of every row block, then one tile
             // at a time: unpack its weights once, use them for every row block
             bf16x8_t av[MB][4];
@@ -270,13 +310,26 @@ __device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, LDS_AS 
     }
 
     // ---- sum the waves, in wave order ----------------------------------------
+    if constexpr (NORM) {
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) ssq += __shfl_xor(ssq, o, 64);
+    }
     __syncthreads();                                     // LDS free for the reduction
     LDS_AS f32x4_t* red = (LDS_AS f32x4_t*)slot[0];
+    LDS_AS float* red_ssq = (LDS_AS float*)(slot[0] + G::WAVES * G::OUT_SLOTS * 16);
 #pragma unroll
     for (int t = 0; t < TILES; t++)
 #pragma unroll
         for (int mb = 0; mb < MB; mb++) red[(wave * TILES * MB + t * MB + mb) * 64 + lane] = acc[t][mb];
+    if (NORM && lane == 0) red_ssq[wave] = ssq;
     __syncthreads();
+    float inv_rms = 1.0f;
+    if constexpr (NORM) {
+        float t = red_ssq[0];
+#pragma unroll
+        for (int q = 1; q < G::WAVES; q++) t += red_ssq[q];   // in wave order
+        inv_rms = 1.0f / sqrtf(t / (float)K + p.norm_eps);
+    }
     constexpr uint32_t TILE_BYTES = G::OUT_SLOTS * 16;
     constexpr int NE = (G::OUT_SLOTS + G::NT - 1) / G::NT;
     const __amdgpu_buffer_rsrc_t rws = make_rsrc((const uint8_t*)p.workspace + (size_t)wg * sk * TILE_BYTES);
@@ -292,6 +345,7 @@ __device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, LDS_AS 
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int q = 0; q < G::WAVES; q++) v[e] += pw[q];   // in wave order
+            if (NORM) v[e] *= inv_rms;
             if (sk > 1) st_agent_x4(rws, part * TILE_BYTES + slot * 16, v[e]);
         }
     }
@@ -314,9 +368,9 @@ __device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, LDS_AS 
     if (sk > 1) reset_counter(&p.semaphores[wg]);
 }
 
-template <int TILES, int MB>
+template <int TILES, int MB, bool NORM = false>
 __device__ __forceinline__ void w4_decode(const t0_w4a16_params& p) {
-    using G = W4DecCfg<TILES, MB>;
+    using G = W4DecCfg<TILES, MB, NORM>;
     // distinct objects, so that the compiler tells the slots' DMAs apart
     __shared__ __attribute__((aligned(1024))) uint8_t slot0[G::SLOT_BYTES];
     __shared__ __attribute__((aligned(1024))) uint8_t slot1[G::SLOTS > 1 ? G::SLOT_BYTES : 16];
@@ -328,11 +382,11 @@ __device__ __forceinline__ void w4_decode(const t0_w4a16_params& p) {
     // zero points and scale type are uniform: one straight-line body each
     const bool zp = p.zeros != nullptr, sf32 = p.flags & T0_W4_SCALE_F32;
     if (zp) {
-        if (sf32) w4_decode_body<TILES, MB, true, true>(p, sl, &s_last);
-        else w4_decode_body<TILES, MB, true, false>(p, sl, &s_last);
+        if (sf32) w4_decode_body<TILES, MB, true, true, NORM>(p, sl, &s_last);
+        else w4_decode_body<TILES, MB, true, false, NORM>(p, sl, &s_last);
     } else {
-        if (sf32) w4_decode_body<TILES, MB, false, true>(p, sl, &s_last);
-        else w4_decode_body<TILES, MB, false, false>(p, sl, &s_last);
+        if (sf32) w4_decode_body<TILES, MB, false, true, NORM>(p, sl, &s_last);
+        else w4_decode_body<TILES, MB, false, false, NORM>(p, sl, &s_last);
     }
 }
 
@@ -642,6 +696,18 @@ T0_W4_DECODE(1, 4)
 T0_W4_DECODE(2, 4)
 T0_W4_DECODE(3, 4)
 T0_W4_DECODE(4, 4)
+
+// t0k_w4a16_decode_norm_t<TILES>: the M == 1 decode with residual add +
+// RMSNorm fused in front (activations from t0_w4a16_params.norm_*).
+#define T0_W4_DECODE_NORM(TILES)                                                                 \
+    extern "C" __global__ void __launch_bounds__(64 * t0_w4_decode_norm_waves(TILES))             \
+        t0k_w4a16_decode_norm_t##TILES(const t0_w4a16_params p) {                                 \
+        t0::w4_decode<TILES, 1, true>(p);                                                        \
+    }
+T0_W4_DECODE_NORM(1)
+T0_W4_DECODE_NORM(2)
+T0_W4_DECODE_NORM(3)
+T0_W4_DECODE_NORM(4)
 
 #define T0_W4_PREFILL(BM, BN, WM, WN, ST)                                                        \
     extern "C" __global__ void __launch_bounds__(WM * WN * 64)                                    \

@@ -57,6 +57,11 @@ class W4A16DescC(C.Structure):
                 ("scales_f32", u32), ("out_f32", u32), ("split_k", u32)]
 
 
+class RmsNormDescC(C.Structure):
+    _fields_ = [("residual", u64), ("hidden", u64), ("gamma", u64), ("x2_out", u64), ("eps", C.c_float),
+                ("pad_", u32)]
+
+
 P = C.POINTER
 SIGNATURES = {
     "t0_last_error": ([], cp), "t0_version": ([], cp),
@@ -140,6 +145,10 @@ SIGNATURES = {
     "t0_bf16_matmul_backward_data": ([vp, u64, u64, u64, u32, u32, u32], C.c_int),
     "t0_bf16_matmul_backward_weight": ([vp, u64, u64, u64, u32, u32, u32], C.c_int),
     "t0_bf16_matmul_with_wt_bf16": ([vp, u64, u64, u64, u32, u32, u32], C.c_int),
+    "t0_ffn_fused_rmsnorm_gemm": ([vp, u64, u64, u64, u64, u64, u32, u32, C.c_float], C.c_int),
+    "t0_rmsnorm": ([vp, u64, u64, u64, u64, u64, u32, u32, u32, C.c_float, C.c_int], C.c_int),
+    "t0_rmsnorm_w4a16": ([vp, P(W4A16DescC), P(RmsNormDescC)], C.c_int),
+    "t0_rmsnorm_matmul": ([vp, u64, u64, u64, u64, u64, u64, u32, u32, u32, C.c_float], C.c_int),
     "t0_graph_begin": ([vp], C.c_int),
     "t0_graph_end": ([vp, P(vp)], C.c_int),
     "t0_graph_launch": ([vp, vp], C.c_int),

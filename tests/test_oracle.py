@@ -15,6 +15,10 @@ Pin map (function -> checks in this file):
                      all-ones, auto_gemm smoke pattern, tile_ir structured
                      pattern); NN == NT on B^T; sequential-order IEEE case
   gemm_rows          equals the full product's rows
+  rmsnorm_rows /     the reference's test_cpu_fused_reference and
+  ffn_fused_*        test_fused_equals_separate; exact closed forms (x2 = 2,
+                     eps 0 / 12) that a dropped term, misplaced eps or gamma
+                     index fails
   bf16_matmul*       int64 products on integer inputs (forward, dX, dW, non-
                      square); RNE tie cases that unrounded operands would fail
   splitk_sum         IEEE order case + integer planes
@@ -244,6 +248,62 @@ def test_bf16_matmul_rounds_operands_rne():
         assert orc.bf16_matmul(x, ones)[0, 0] == np.float32(k * want)
         assert orc.bf16_matmul(ones.T.copy(), x.T.copy())[0, 0] == np.float32(k * want)
         assert orc.bf16_matmul_backward_weight(x.T.copy(), np.ones((k, 1), np.float32))[0, 0] == np.float32(k * want)
+
+
+def _sin_data(n, f, scale=1.0, op=np.sin):
+    return (op(np.arange(n, dtype=np.float32) * np.float32(f)) * np.float32(scale)).astype(np.float32)
+
+
+def test_ffn_fused_reference_test_vectors():
+    """src/t0/ffn_fused_kernels.rs:247-299 (test_cpu_fused_reference): the
+    fused result equals the step-by-step row-0 computation, and RMSNorm
+    leaves rms(x2 * inv_rms) = 1."""
+    m, d, eps = 2, 64, 1e-5
+    res = _sin_data(m * d, 0.17).reshape(m, d)
+    hid = _sin_data(m * d, 0.23, op=np.cos).reshape(m, d)
+    gamma = (0.8 + np.arange(d, dtype=np.float32) * np.float32(0.005)).astype(np.float32)
+    w = _sin_data(m * d, 0.31, 0.5).reshape(m, d)
+    out = orc.ffn_fused_rmsnorm_gemm(res, hid, gamma, w, eps)
+    x2 = (res[0] + hid[0]).astype(np.float64)
+    inv = 1.0 / np.sqrt((x2 * x2).sum() / d + eps)
+    assert abs(out[0] - float(((x2 * inv * gamma) * w[0]).sum())) < 1e-4
+    _, x2o, invo = orc.rmsnorm_rows(res, hid, np.ones(d, np.float32), eps)
+    normed = x2o[0].astype(np.float64) * float(invo[0])
+    assert abs(np.sqrt((normed ** 2).mean()) - 1.0) < 1e-4
+
+
+def test_ffn_fused_equals_separate():
+    """src/t0/ffn_fused_kernels.rs:318-381 (test_fused_equals_separate): the
+    fused kernel's CPU form equals residual add, then cpu_rmsnorm_forward,
+    then the per-row dot, within 1e-4."""
+    m, d, eps = 4, 128, 1e-5
+    res = _sin_data(m * d, 0.13, 1.5).reshape(m, d)
+    hid = _sin_data(m * d, 0.19, 0.8, op=np.cos).reshape(m, d)
+    gamma = (0.9 + np.arange(d, dtype=np.float32) * np.float32(0.002)).astype(np.float32)
+    w = _sin_data(m * d, 0.41).reshape(m, d)
+    fused = orc.ffn_fused_rmsnorm_gemm(res, hid, gamma, w, eps)
+    normed, _, _ = orc.rmsnorm_rows(res + hid, None, gamma, eps)
+    separate = (normed * w).sum(axis=1, dtype=np.float32)
+    assert np.max(np.abs(fused - separate)) < 1e-4
+
+
+@pytest.mark.parametrize("eps,scale", [(0.0, 1.0), (12.0, 0.5)])
+def test_rmsnorm_closed_forms(eps, scale):
+    """residual = [3, -1, ...], hidden = [-1, 3, ...] gives x2 = 2 everywhere:
+    mean(x2^2) = 4, so inv_rms = 1/2 (eps 0) or 1/4 (eps 12, added before the
+    root) and normed = scale * gamma exactly.  A dropped hidden term (rms of
+    [3, -1] is sqrt(5)), eps added after the root, or a shifted gamma index
+    all miss these values."""
+    m, d = 3, 40
+    res = np.tile(np.array([3.0, -1.0], np.float32), (m, d // 2))
+    hid = np.tile(np.array([-1.0, 3.0], np.float32), (m, d // 2))
+    gamma = (np.arange(d) % 5 + 1).astype(np.float32)
+    normed, x2, inv = orc.rmsnorm_rows(res, hid, gamma, eps)
+    assert np.all(x2 == 2.0) and np.all(inv == np.float32(scale / 2))
+    assert np.array_equal(normed, np.tile(gamma * np.float32(scale), (m, 1)))
+    w = (np.arange(m * d) % 7 - 3).reshape(m, d).astype(np.float32)
+    out = orc.ffn_fused_rmsnorm_gemm(res, hid, gamma, w, eps)
+    assert np.array_equal(out, (scale * (gamma[None, :] * w).sum(axis=1)).astype(np.float32))
 
 
 def test_splitk_sum():
