@@ -258,6 +258,51 @@ def bench_ignis(rt, steps, warmup, rng, tr):
             "tflops_backward": round(2 * fl / (ms_b * 1e-3) / 1e12, 1)}
 
 
+def bench_norm_decode(rt, steps, warmup, rng, tr):
+    """One decode token through residual add + RMSNorm + the W4A16 projection
+    (M=1, K=4096, N=11008, g=128, z=8): the fused decode kernel against the
+    two-kernel path (RMSNorm to bf16, then the decode GEMM), 12 rotated
+    weight sets as graph replays."""
+    from t0_gpu._ffi import RmsNormDescC, W4A16DescC
+    import ctypes as C
+    m, n, k, gs = 1, 11008, 4096, 128
+    res = rt.upload(rng.standard_normal((m, k), dtype=np.float32))
+    hid = rt.upload(rng.standard_normal((m, k), dtype=np.float32))
+    gam = rt.upload(rng.uniform(0.5, 1.5, k).astype(np.float32))
+    x2 = rt.alloc(4 * k)
+    a16 = rt.alloc(2 * k)
+    sets = []
+    for _ in range(ROTATE):
+        qw, s, _ = _w4_operands(rng, n, k, gs, False)
+        sets.append((rt.upload(qw), rt.upload(s)))
+    dc = rt.alloc(m * n * 2)
+    L = t0.lib()
+    nd = RmsNormDescC(residual=res.gpu_addr(), hidden=hid.gpu_addr(), gamma=gam.gpu_addr(), x2_out=x2.gpu_addr(),
+                      eps=1e-5)
+
+    def fused(i):
+        d = W4A16DescC(a=0, qweight=sets[i][0].gpu_addr(), scales=sets[i][1].gpu_addr(), zeros=0, c=dc.gpu_addr(),
+                       m=m, n=n, k=k, group_size=gs, zero_const=8)
+        t0._check(L.t0_rmsnorm_w4a16(rt.h, C.byref(d), C.byref(nd)))
+
+    def separate(i):
+        t0._check(L.t0_rmsnorm(rt.h, res.gpu_addr(), hid.gpu_addr(), gam.gpu_addr(), a16.gpu_addr(), x2.gpu_addr(),
+                               1, k, k, 1e-5, 1))
+        rt.w4a16(a16.gpu_addr(), sets[i][0].gpu_addr(), sets[i][1].gpu_addr(), 0, dc.gpu_addr(), m, n, k,
+                 group_size=gs, zero_const=8)
+
+    fused(0)
+    separate(0)
+    rt.wait_idle()
+    ms_f = rotate_timed(rt, fused, steps, warmup)
+    ms_s = rotate_timed(rt, separate, steps, warmup)
+    for buf in [res, hid, gam, x2, a16, dc] + [b for st in sets for b in st]:
+        buf.free()
+    return {"workload": "decode token: residual + RMSNorm + W4A16 M=1 K=4096 N=11008, g=128, z=8",
+            "kernel": "t0k_w4a16_decode_norm_t3", "us_fused": round(ms_f * 1e3, 3),
+            "us_two_kernels": round(ms_s * 1e3, 3)}
+
+
 def cpu_baseline(a, b, rows: int):
     """The reference CPU matmul (oracle restatement, one thread) on rows
     [0, rows) of the 4096^3 product, scaled to the whole product."""
@@ -284,7 +329,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="issue rotated launches directly (for tracers)")
-    ap.add_argument("--only", choices=["gemm4096", "skinny", "decode", "prefill", "ignis", "copy"], default=None,
+    ap.add_argument("--only", choices=["gemm4096", "skinny", "decode", "prefill", "ignis", "norm_decode", "copy"],
+                    default=None,
                     help="run one workload (for counter collection)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -301,7 +347,8 @@ def main():
 
     if args.only:
         fn = {"gemm4096": bench_gemm_4096, "skinny": bench_skinny, "decode": bench_decode,
-              "prefill": bench_prefill, "ignis": bench_ignis, "copy": bench_copy}[args.only]
+              "prefill": bench_prefill, "ignis": bench_ignis, "norm_decode": bench_norm_decode,
+              "copy": bench_copy}[args.only]
         r = fn(rt, args.steps, args.warmup, rng, tr)
         r.pop("a", None)
         r.pop("b", None)
@@ -315,7 +362,7 @@ def main():
     extras = {}
     if not args.no_extras:
         for name, fn in (("skinny", bench_skinny), ("w4a16_decode", bench_decode), ("w4a16_prefill", bench_prefill),
-                         ("ignis_matmul", bench_ignis)):
+                         ("ignis_matmul", bench_ignis), ("norm_decode", bench_norm_decode)):
             extras[name] = fn(rt, args.steps, args.warmup, rng, tr)
             print(f"# {name}: {json.dumps(extras[name])}", file=sys.stderr, flush=True)
     cpu = None

@@ -136,6 +136,7 @@ int ensure_sem(t0_runtime* rt, size_t count) {
 }
 
 bool aligned16(uint64_t p) { return (p & 15) == 0; }
+bool aligned8(uint64_t p) { return (p & 7) == 0; }
 
 // Fast tiled kernels need 16-byte operand rows; anything else takes the
 // generic kernel.  NN reads B in 8-column chunks: with N % 8 != 0 the last
@@ -1359,8 +1360,6 @@ int t0_bf16_matmul_with_wt_bf16(t0_runtime* rt, uint64_t x, uint64_t wt, uint64_
 // (src/ignis/ops/fused_rmsnorm_gemm.rs) with an INT4 or a dense weight.
 namespace {
 
-bool aligned8(uint64_t p) { return (p & 7) == 0; }
-
 int launch_rmsnorm(t0_runtime* rt, uint64_t res, uint64_t hid, uint64_t gamma, uint64_t out, uint64_t x2_out,
                    uint32_t rows, uint32_t d, uint32_t ld_out, float eps, bool out_bf16) {
     hipFunction_t f;
@@ -1371,6 +1370,11 @@ int launch_rmsnorm(t0_runtime* rt, uint64_t res, uint64_t hid, uint64_t gamma, u
     p.res = (const float*)res; p.hid = (const float*)hid; p.gamma = (const float*)gamma;
     p.out = (void*)out; p.x2_out = (float*)x2_out;
     p.rows = rows; p.d = d; p.ld_out = ld_out; p.out_bf16 = out_bf16; p.eps = eps;
+    // 16-byte chunks: rows of a multiple of 4 elements, every row start 16-byte
+    // aligned on the inputs and 8/16-byte aligned on the output
+    const bool vec = d % 4 == 0 && ld_out % 4 == 0 && aligned16(res) && aligned16(hid) && aligned16(gamma) &&
+                     aligned16(x2_out) && (out_bf16 ? aligned8(out) : aligned16(out));
+    p.flags = vec ? T0_RMSNORM_VEC4 : 0;
     return launch(rt, f, rows, 1, 1, 256, p);
 }
 

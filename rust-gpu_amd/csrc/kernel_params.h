@@ -103,8 +103,9 @@ typedef struct t0_rmsnorm_params {
     uint32_t ld_out;          // elements
     uint32_t out_bf16;
     float eps;
-    uint32_t pad_;
+    uint32_t flags;           // T0_RMSNORM_VEC4: 16-byte rows and pointers
 } t0_rmsnorm_params;
+#define T0_RMSNORM_VEC4 0x1u
 
 // Reference dequant kernel arguments (src/t0/quant_kernels.rs:45-47):
 // [packed_weights, scales(f32), zero_points(i32), output; rows, cols]

@@ -191,21 +191,70 @@ __device__ __forceinline__ void ffn_fused_rmsnorm_gemm(const t0_ffn_params& p) {
 __device__ __forceinline__ void rmsnorm_rows(const t0_rmsnorm_params& p) {
     __shared__ float sh[4];
     const uint32_t d = p.d, t = threadIdx.x, r = blockIdx.x;
-    const size_t base = (size_t)r * d;
+    const float* __restrict__ res = p.res + (size_t)r * d;
+    const float* __restrict__ hid = p.hid ? p.hid + (size_t)r * d : nullptr;
+    float* __restrict__ x2o = p.x2_out ? p.x2_out + (size_t)r * d : nullptr;
+    const size_t ob = (size_t)r * p.ld_out;
     float ssq = 0.0f;
-    for (uint32_t i = t; i < d; i += 256) {
-        const float x2 = p.hid ? p.res[base + i] + p.hid[base + i] : p.res[base + i];
-        if (p.x2_out) p.x2_out[base + i] = x2;
-        ssq += x2 * x2;
+    if (p.flags & T0_RMSNORM_VEC4) {
+        // 16-byte chunks, four per lane in flight: a 4096-wide row is one round
+        const uint32_t nc = d / 4;
+        for (uint32_t c0 = t; c0 < nc; c0 += 1024) {
+            f32x4_t v[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const uint32_t c = c0 + 256 * u;
+                v[u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+                if (c < nc) {
+                    v[u] = *(const f32x4_t*)(res + 4 * c);
+                    if (hid) v[u] += *(const f32x4_t*)(hid + 4 * c);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const uint32_t c = c0 + 256 * u;
+                if (c < nc && x2o) *(f32x4_t*)(x2o + 4 * c) = v[u];
+#pragma unroll
+                for (int e = 0; e < 4; e++) ssq += v[u][e] * v[u][e];
+            }
+        }
+    } else {
+#pragma unroll 4
+        for (uint32_t i = t; i < d; i += 256) {
+            const float x2 = hid ? res[i] + hid[i] : res[i];
+            if (x2o) x2o[i] = x2;
+            ssq += x2 * x2;
+        }
     }
     ssq = block_sum<4>(ssq, sh);
     const float inv_rms = 1.0f / sqrtf(ssq / (float)d + p.eps);
-    const size_t ob = (size_t)r * p.ld_out;
-    for (uint32_t i = t; i < d; i += 256) {
-        const float x2 = p.hid ? p.res[base + i] + p.hid[base + i] : p.res[base + i];
-        const float y = (x2 * inv_rms) * p.gamma[i];
-        if (p.out_bf16) ((uint16_t*)p.out)[ob + i] = (uint16_t)(pack2_bf16_rne(y, 0.f) & 0xFFFFu);
-        else ((float*)p.out)[ob + i] = y;
+    if (p.flags & T0_RMSNORM_VEC4) {
+        const uint32_t nc = d / 4;
+        for (uint32_t c0 = t; c0 < nc; c0 += 1024) {
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const uint32_t c = c0 + 256 * u;
+                if (c >= nc) continue;
+                f32x4_t x = *(const f32x4_t*)(res + 4 * c);
+                if (hid) x += *(const f32x4_t*)(hid + 4 * c);
+                const f32x4_t g = *(const f32x4_t*)(p.gamma + 4 * c);
+                f32x4_t y;
+#pragma unroll
+                for (int e = 0; e < 4; e++) y[e] = (x[e] * inv_rms) * g[e];
+                if (p.out_bf16)
+                    *(u32x2_t*)((uint16_t*)p.out + ob + 4 * c) = u32x2_t{pack2_bf16_rne(y[0], y[1]), pack2_bf16_rne(y[2], y[3])};
+                else
+                    *(f32x4_t*)((float*)p.out + ob + 4 * c) = y;
+            }
+        }
+    } else {
+#pragma unroll 4
+        for (uint32_t i = t; i < d; i += 256) {
+            const float x2 = hid ? res[i] + hid[i] : res[i];
+            const float y = (x2 * inv_rms) * p.gamma[i];
+            if (p.out_bf16) ((uint16_t*)p.out)[ob + i] = (uint16_t)(pack2_bf16_rne(y, 0.f) & 0xFFFFu);
+            else ((float*)p.out)[ob + i] = y;
+        }
     }
     for (uint32_t i = d + t; i < p.ld_out; i += 256) {   // a padded row: zeros after the data
         if (p.out_bf16) ((uint16_t*)p.out)[ob + i] = 0;

@@ -90,7 +90,8 @@ def test_ffn_fused_raw_dispatch_with_reference_kernargs(rt):
 
 
 @pytest.mark.parametrize("rows,d,with_hid,out_bf16", [(1, 4096, True, True), (5, 1000, False, False),
-                                                      (3, 64, True, False), (16, 4096, True, True)])
+                                                      (3, 64, True, False), (16, 4096, True, True),
+                                                      (2, 1001, True, True), (1, 9000, False, False)])
 def test_rmsnorm_rows(rt, rows, d, with_hid, out_bf16):
     rng = np.random.default_rng(rows * 10 + d)
     res = rng.standard_normal((rows, d)).astype(np.float32)
@@ -187,7 +188,7 @@ def test_fused_rmsnorm_w4a16_closed_form(rt, zp):
         b.free()
 
 
-@pytest.mark.parametrize("m,k,n,with_hid", [(1, 300, 130, True), (7, 512, 256, False), (33, 1000, 520, True)])
+@pytest.mark.parametrize("m,k,n,with_hid", [(1, 301, 130, True), (7, 512, 256, False), (33, 1000, 520, True)])
 def test_fused_residual_rmsnorm_gemm_dense(rt, m, k, n, with_hid):
     """Dense f32 weight [k, n]: RMSNorm then the bf16 matmul (the Ignis
     prefill branch), bf16(normed) . bf16(W) in f32; k and n not multiples of 8."""
