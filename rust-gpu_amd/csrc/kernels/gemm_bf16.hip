@@ -422,15 +422,36 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
             }
     __shared__ uint32_t s_last;
     if (!publish_and_count(&p.semaphores[tile_id], sk, &s_last)) return;
+    // The lane's NOUT 16-byte outputs are summed over the planes in plane
+    // order; the loads of up to 32 (output, plane) pairs go out before any is
+    // consumed (planes past split_k are not loaded).
+    constexpr int NJ = G::FN * 4, NOUT = G::FM * NJ;
+    constexpr int QB = NOUT >= 32 ? 1 : 32 / NOUT;   // planes per batch
+    f32x4_t v[NOUT];
+#pragma unroll
+    for (int o = 0; o < NOUT; o++) v[o] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll 1
-    for (uint32_t i = 0; i < (uint32_t)G::FM; i++) {
-#pragma unroll 1
-        for (uint32_t jg = 0; jg < (uint32_t)G::FN * 4; jg++) {
-            const uint32_t j = jg / 4, g = jg % 4;
-            const uint32_t idx = (i * G::FN * 4 + jg) * G::NT + tid;
-            const f32x4_t v = sum_partials_x4(rws, idx * 16, TILE_BYTES, sk);
-            *(LDS_AS f32x4_t*)(wreg + l32 * G::EPI_LD + j * 32 + 8 * g + 4 * hi) = v;
+    for (uint32_t q0 = 0; q0 < sk; q0 += QB) {
+        f32x4_t t[NOUT][QB];
+#pragma unroll
+        for (int qq = 0; qq < QB; qq++) {
+            if (q0 + qq >= sk) break;                    // uniform
+#pragma unroll
+            for (int o = 0; o < NOUT; o++)
+                t[o][qq] = ld_agent_x4(rws, ((uint32_t)o * G::NT + tid) * 16 + (q0 + qq) * TILE_BYTES);
         }
+#pragma unroll
+        for (int qq = 0; qq < QB; qq++) {
+            if (q0 + qq >= sk) break;
+#pragma unroll
+            for (int o = 0; o < NOUT; o++) v[o] += t[o][qq];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < G::FM; i++) {
+#pragma unroll
+        for (int jg = 0; jg < NJ; jg++)
+            *(LDS_AS f32x4_t*)(wreg + l32 * G::EPI_LD + (jg / 4) * 32 + 8 * (jg % 4) + 4 * hi) = v[i * NJ + jg];
         emit_rowblock<G>(p, Cb, wreg, row_base + i * 32, col_base, lane);
     }
     reset_counter(&p.semaphores[tile_id]);
