@@ -181,6 +181,21 @@ def test_auto_select_sizes():
     assert (c.tile_m, c.tile_n) == (256, 256)
 
 
+def test_auto_select_takes_measured_best_on_llm_shapes():
+    """Shapes whose every tile x split candidate was timed on MI355X (NN,
+    bf16 out): the selection is the measured fastest, and it splits K only
+    where one partition per tile cannot fill the 256 CUs.
+    (M, N, K) -> (tile_m, tile_n, split, threads)."""
+    cases = {(4096, 11008, 4096): (256, 256, 1, 512), (4096, 4096, 11008): (256, 256, 1, 512),
+             (2048, 11008, 4096): (256, 256, 1, 512), (1024, 11008, 4096): (256, 256, 1, 512),
+             (1024, 4096, 4096): (128, 128, 1, 256), (4096, 1024, 4096): (128, 128, 1, 256),
+             (256, 11008, 4096): (128, 128, 1, 256), (256, 4096, 4096): (64, 128, 2, 256),
+             (4096, 4096, 1024): (256, 256, 1, 512)}
+    for (m, n, k), want in cases.items():
+        c = t0.auto_select(m, k, n)
+        assert (c.tile_m, c.tile_n, max(c.split_k, 1), c.wg_size) == want, ((m, n, k), c.name())
+
+
 def test_auto_select_legacy_preserved():
     """src/t0/gemm_gen.rs:606-617."""
     c = t0.auto_select_legacy(256, 256, 256)
