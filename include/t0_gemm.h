@@ -141,7 +141,8 @@ int t0_build_kernargs_backward_weight(uint64_t dy_t, uint64_t x_t, uint64_t dw, 
 
 /* --------------------------------------------------------- auto-selection */
 /* Replaces auto_select (src/t0/gemm_gen.rs:340-342 -> cost_model::predict_best,
- * src/t0/cost_model.rs:660-668) with a gfx950 model.  Note argument order (m, k, n). */
+ * src/t0/cost_model.rs:660-668) with a per-tile cost table measured on MI355X
+ * (tile x split-K ranked by predicted time).  Note argument order (m, k, n). */
 int t0_auto_select(uint32_t m, uint32_t k, uint32_t n, t0_gemm_config* out);
 /* Replaces auto_select_legacy (src/t0/gemm_gen.rs:351-404): the reference's
  * decision tree over the shapes, mapped onto gfx950 tiles. */
