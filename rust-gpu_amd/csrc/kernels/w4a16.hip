@@ -9,35 +9,21 @@
 //                             or none, with a constant zero point.
 //   w(n,k) = (q(n,k) - z(n,g)) * s(n,g)      (src/t0/quant_kernels.rs:365-372)
 //
-// Fused dequant, exact: a nibble pair becomes two bf16 of value
-// 144 + q - z (an integer in [129,159], exact in bf16) with one v_perm and one
-// integer add; MFMA accumulates T = sum a*(144 + q - z) over a quant group;
-// the group's result is s * (T - 144 * sum a), applied in f32.  So the weight
-// value the GEMM uses is exactly (q - z) * s and the weights cross HBM once, at
-// 4 bits.
+// Fused dequant, exact: a nibble pair becomes two bf16 of value 128 + q (an
+// integer in [128,143], exact in bf16) with one v_perm and one v_and_or; MFMA
+// accumulates T = sum a*(128 + q) - (128 + z) * sum a over a quant group (the
+// zero-point term from the activations' row sums: per decode tile, or as one
+// more MFMA block in the prefill); the group's result s * T is applied in f32.
+// So the weight value the GEMM uses is exactly (q - z) * s and the weights
+// cross HBM once, at 4 bits.
 #include "common.h"
 
 namespace t0 {
-
-// 8 nibbles of one u32 (k = 0..7) -> 8 bf16 of (144 + q - z), as 4 u32 pairs.
-// kadd = 0x43004300 + (16 - z) * 0x00010001.
-T0_DEV bf16x8_t unpack8(uint32_t w, uint32_t kadd) {
-    const uint32_t lo = w & 0x0F0F0F0Fu;          // bytes q0 q2 q4 q6
-    const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;   // bytes q1 q3 q5 q7
-    u32x4_t r;
-    r[0] = __builtin_amdgcn_perm(hi, lo, 0x0C040C00u) + kadd;   // q0 | q1<<16
-    r[1] = __builtin_amdgcn_perm(hi, lo, 0x0C050C01u) + kadd;   // q2 | q3<<16
-    r[2] = __builtin_amdgcn_perm(hi, lo, 0x0C060C02u) + kadd;   // q4 | q5<<16
-    r[3] = __builtin_amdgcn_perm(hi, lo, 0x0C070C03u) + kadd;   // q6 | q7<<16
-    return __builtin_bit_cast(bf16x8_t, r);
-}
 
 T0_DEV uint32_t zero_of(const t0_w4a16_params& p, uint32_t g, uint32_t n) {
     if (!p.zeros) return p.zero_const;
     return (p.zeros[(size_t)g * (p.N / 8) + n / 8] >> (4 * (n % 8))) & 0xFu;
 }
-
-T0_DEV uint32_t kadd_of(uint32_t z) { return 0x43004300u + (16u - z) * 0x00010001u; }
 
 T0_DEV float scale_of(const t0_w4a16_params& p, uint32_t g, uint32_t n) {
     const size_t i = (size_t)g * p.N + n;
@@ -397,12 +383,18 @@ __device__ __forceinline__ void w4_decode(const t0_w4a16_params& p) {
 //     A  [BM][128] bf16, 16-B chunks swizzled by row         BM*256 B
 //     W  [BN][16 words] packed nibbles, chunk-swizzled         BN*64 B
 //     S  [BN] bf16 scales of this group                        BN*2 B (padded to 1 KB slot)
-//     X  [BM] f32: -144 * sum_k a[m][k] over this group        BM*4 B
+//     R  [BM] f32: sum_k a[m][k] over this group                BM*4 B
 //   MFMA step kk (0..7) takes, in lane half h, the 8 k of word h*8 + kk, so a
 //   lane reads its W column as two 16-B LDS loads per group.
-//   Per group: T = sum_kk mfma(unpack(W), A);  acc += s_n * (T + X_m).
+//   Per group T = sum_k a[m][k] * (q[k][n] - z_n), exactly as MFMA products:
+//     - the nibbles unpack to bf16 128 + q (exact);
+//     - one more 16-deep MFMA block per group holds the correction
+//       -(128 + z_n) * R_m: its A rows are R_m split into three bf16 pieces
+//       (hi + mid + lo == R_m exactly), its B columns -(128 + z_n) three
+//       times (an exact bf16 integer), the other 13 k zero;
+//   then acc += s_n * T, one FMA per output per group.
 // Requires: group_size == 128, K % 128 == 0, lda % 8 == 0, N % 8 == 0,
-//           X precomputed by w4_rowsum into workspace [G][M].
+//           R precomputed by w4_rowsum into workspace [G][M].
 // ---------------------------------------------------------------------------
 template <int CH>
 T0_DEV uint32_t swz16(uint32_t r) { return r & (CH - 1) & 15; }
@@ -512,6 +504,7 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
     // W operand: column wn*TN + j*32 + l32, words h*8..h*8+7 = chunks 2h, 2h+1
     const uint32_t w_sw = ((l32 >> 1) ^ (l32 >> 3)) & 3;
     const uint32_t w_c0 = ((2 * h) ^ w_sw) * 16, w_c1 = ((2 * h + 1) ^ w_sw) * 16;
+    const uint32_t bits4300 = __builtin_amdgcn_mov_dpp(0x43004300u, 0xE4, 0xF, 0xF, false);  // in a VGPR
 
 #pragma unroll
     for (int s = 0; s < STAGES - 1; s++)
@@ -529,9 +522,10 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
         const LDS_AS uint32_t* sz = (const LDS_AS uint32_t*)(st + G::A_BYTES + G::W_BYTES + G::Z_OFF);
         const LDS_AS float* sx = (const LDS_AS float*)(st + G::A_BYTES + G::W_BYTES + G::S_BYTES);
 
-        // this lane's W words and zero-point adders for the group
+        // this lane's W words, and the correction block's operands: B column
+        // -(128 + z) in k 0..2 of lane half 0, A row R split hi/mid/lo likewise
         u32x4_t wlo[G::FN], whi[G::FN];
-        uint32_t kadd[G::FN];
+        bf16x8_t zcol[G::FN], rrow[G::FM];
 #pragma unroll
         for (int j = 0; j < G::FN; j++) {
             const uint32_t col = wn * G::TN + j * 32 + l32;
@@ -539,9 +533,24 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
             wlo[j] = *(const LDS_AS u32x4_t*)(wr + w_c0);
             whi[j] = *(const LDS_AS u32x4_t*)(wr + w_c1);
             const uint32_t z = p.zeros ? (sz[col / 8] >> (4 * (col % 8))) & 0xFu : p.zero_const;
-            kadd[j] = kadd_of(z);
+            const uint32_t zb = h ? 0u : 0xC300u + z;                     // bf16 -(128 + z)
+            zcol[j] = __builtin_bit_cast(bf16x8_t, u32x4_t{zb | (zb << 16), zb, 0u, 0u});
+        }
+#pragma unroll
+        for (int i = 0; i < G::FM; i++) {
+            const float r = h ? 0.0f : sx[wm * G::TM + i * 32 + l32];
+            const uint32_t hi = __float_as_uint(r) & 0xFFFF0000u;
+            const float r1 = r - __uint_as_float(hi);                       // exact
+            const uint32_t mid = __float_as_uint(r1) & 0xFFFF0000u;
+            const uint32_t lo = __float_as_uint(r1 - __uint_as_float(mid)); // <= 8 significant bits: exact in bf16
+            rrow[i] = __builtin_bit_cast(bf16x8_t, u32x4_t{(hi >> 16) | mid, lo >> 16, 0u, 0u});
         }
         f32x16_t tmp[G::FM][G::FN];
+#pragma unroll
+        for (int i = 0; i < G::FM; i++)
+#pragma unroll
+            for (int j = 0; j < G::FN; j++)
+                tmp[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(zcol[j], rrow[i], f32x16_t{}, 0, 0, 0);
 #pragma unroll
         for (int kk = 0; kk < 8; kk++) {
             bf16x8_t af[G::FM], bw[G::FN];
@@ -551,17 +560,14 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
                 af[i] = *(const LDS_AS bf16x8_t*)(sa + a_row0 + i * 32 * 256 + c * 16);
             }
 #pragma unroll
-            for (int j = 0; j < G::FN; j++) bw[j] = unpack8(kk < 4 ? wlo[j][kk] : whi[j][kk - 4], kadd[j]);
+            for (int j = 0; j < G::FN; j++) bw[j] = unpack8_128(kk < 4 ? wlo[j][kk] : whi[j][kk - 4], bits4300);
 #pragma unroll
             for (int i = 0; i < G::FM; i++)
 #pragma unroll
                 for (int j = 0; j < G::FN; j++)
-                    tmp[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[j], af[i], kk == 0 ? f32x16_t{} : tmp[i][j], 0, 0, 0);
+                    tmp[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[j], af[i], tmp[i][j], 0, 0, 0);
         }
-        // acc += s_n * (T + X_m)
-        float xm[G::FM];
-#pragma unroll
-        for (int i = 0; i < G::FM; i++) xm[i] = sx[wm * G::TM + i * 32 + l32];
+        // acc += s_n * T
 #pragma unroll
         for (int j = 0; j < G::FN; j++) {
 #pragma unroll
@@ -572,10 +578,10 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
                 const float s2 = __uint_as_float(sv[1] << 16), s3 = __uint_as_float(sv[1] & 0xFFFF0000u);
 #pragma unroll
                 for (int i = 0; i < G::FM; i++) {
-                    acc[i][j][4 * q4 + 0] = fmaf(s0, tmp[i][j][4 * q4 + 0] + xm[i], acc[i][j][4 * q4 + 0]);
-                    acc[i][j][4 * q4 + 1] = fmaf(s1, tmp[i][j][4 * q4 + 1] + xm[i], acc[i][j][4 * q4 + 1]);
-                    acc[i][j][4 * q4 + 2] = fmaf(s2, tmp[i][j][4 * q4 + 2] + xm[i], acc[i][j][4 * q4 + 2]);
-                    acc[i][j][4 * q4 + 3] = fmaf(s3, tmp[i][j][4 * q4 + 3] + xm[i], acc[i][j][4 * q4 + 3]);
+                    acc[i][j][4 * q4 + 0] = fmaf(s0, tmp[i][j][4 * q4 + 0], acc[i][j][4 * q4 + 0]);
+                    acc[i][j][4 * q4 + 1] = fmaf(s1, tmp[i][j][4 * q4 + 1], acc[i][j][4 * q4 + 1]);
+                    acc[i][j][4 * q4 + 2] = fmaf(s2, tmp[i][j][4 * q4 + 2], acc[i][j][4 * q4 + 2]);
+                    acc[i][j][4 * q4 + 3] = fmaf(s3, tmp[i][j][4 * q4 + 3], acc[i][j][4 * q4 + 3]);
                 }
             }
         }
@@ -603,7 +609,7 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
     }
 }
 
-// X[g][m] = -144 * sum_{k in group g} a[m][k]   (prefill pre-pass, group 128)
+// R[g][m] = sum_{k in group g} a[m][k]   (prefill pre-pass, group 128)
 __device__ __forceinline__ void w4_rowsum(const t0_w4a16_params& p) {
     // one wave per (m, 8 groups): lane covers 16 k of a group
     const uint32_t lane = threadIdx.x & 63;
@@ -626,7 +632,7 @@ __device__ __forceinline__ void w4_rowsum(const t0_w4a16_params& p) {
     s += __shfl_xor(s, 1);
     s += __shfl_xor(s, 2);
     s += __shfl_xor(s, 4);
-    if (g < G && (lane % 8) == 0) p.workspace[(size_t)g * p.M + m] = -144.0f * s;
+    if (g < G && (lane % 8) == 0) p.workspace[(size_t)g * p.M + m] = s;
 }
 
 // Generic W4A16 (any M, N, group size dividing K): one thread per output,

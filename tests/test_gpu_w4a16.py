@@ -188,6 +188,33 @@ def test_w4a16_prefill(rt, dev, m, n):
     check_close(got, ref, w4_tol(a, qw, s, zw, 0, n, k, gs), f"prefill {m}x{n}")
 
 
+@pytest.mark.parametrize("per_group_zeros", [True, False])
+def test_w4a16_prefill_exact_integers(rt, dev, per_group_zeros):
+    """Integer activations in [-3, 3] and power-of-two scales: every group's
+    sum a*(q - z) is an integer below 2^13 and the scaled sum over groups is
+    exact in f32, so the f32 output must equal the exact product bit for bit
+    (the zero-point term enters as one more MFMA block of row sums)."""
+    rng = np.random.default_rng(71 + per_group_zeros)
+    m, n, k, gs = 320, 256, 512, 128
+    G = k // gs
+    qw, _, zw = make_w4(rng, n, k, gs, per_group_zeros=per_group_zeros)
+    s = bf16(2.0 ** rng.integers(-8, -4, (G, n)).astype(np.float32))
+    ai = rng.integers(-3, 4, (m, k))
+    a = bf16(ai.astype(np.float32))
+    zc = 8
+    q = ((qw[:, :, None] >> (4 * np.arange(8, dtype=np.uint32))) & 0xF).reshape(n, k).astype(np.int64)
+    if per_group_zeros:
+        z = np.stack([(zw[:, j // 8] >> (4 * (j % 8))) & 0xF for j in range(n)], axis=1).astype(np.int64)  # [G, n]
+    else:
+        z = np.full((G, n), zc, np.int64)
+    w = (q - np.repeat(z.T, gs, axis=1)) * np.repeat(f32(s).astype(np.float64).T, gs, axis=1)   # [n, k]
+    ref = (ai.astype(np.float64) @ w.T).astype(np.float32)
+    plan, _ = rt.w4a16_plan(0, 0, 0, 0, 0, m, n, k, group_size=gs)
+    assert plan.startswith("t0k_w4a16_prefill")
+    got = run_w4(rt, dev, a, qw, s, zw, m, n, k, gs, zc=zc, out_f32=True)
+    assert np.array_equal(got, ref)
+
+
 def test_w4a16_prefill_headline_rows(rt, dev):
     """4096x4096x14336, per-group zero points; sampled rows."""
     rng = np.random.default_rng(45)
