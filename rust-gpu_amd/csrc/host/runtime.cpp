@@ -1079,12 +1079,11 @@ static int w4_plan(t0_runtime* rt, const t0_w4a16_desc* d, W4Plan& pl) {
     }
     if (fast && M > 64 && N % 8 == 0 && !d->scales_f32) {
         const bool big = M >= 1024;
-        pl.bm = big ? 256 : 128;
-        pl.bn = 128;
+        pl.bm = 128;
+        pl.bn = big ? 256 : 128;
         char b[64];
-        // 256-row tiles on 8 waves (two per SIMD: 4096x4096x14336 576 us vs
-        // 664 us on 4 waves), 128-row tiles on 4
-        snprintf(b, sizeof b, big ? "t0k_w4a16_prefill_%ux%u_w4x2_s2" : "t0k_w4a16_prefill_%ux%u_w2x2_s2", pl.bm,
+        // 128x256 tiles on 8 waves with three stages in LDS, 128x128 on 4
+        snprintf(b, sizeof b, big ? "t0k_w4a16_prefill_%ux%u_w2x4_s3" : "t0k_w4a16_prefill_%ux%u_w2x2_s2", pl.bm,
                  pl.bn);
         pl.sym = b;
         pl.gx = ((M + pl.bm - 1) / pl.bm) * ((N + pl.bn - 1) / pl.bn);

@@ -420,7 +420,11 @@ struct W4Cfg {
     static_assert(BN * 2 <= Z_OFF && BM * 4 <= 1024 * 2, "S/Z/X slots");
     static_assert(NW >= 3, "S, Z and X DMAs go out from three different waves");
     static_assert(SMEM <= 160 * 1024, "LDS");
-    static_assert(NW >= 2 && STAGES == 2, "scale/X DMA split over two waves; vmcnt(0) per stage");
+    static_assert(STAGES == 2 || STAGES == 3, "stage waits below");
+    // loads every wave issues per stage; waves 0, 1 and NW-1 add the scale,
+    // zero-point and row-sum DMAs, so a wait for MIN_LOADS outstanding covers
+    // one stage in flight on every wave (a wave with extras waits slightly longer)
+    static constexpr int MIN_LOADS = A_LOADS + W_LOADS;
 };
 
 template <int BM, int BN, int WM, int WN, int STAGES>
@@ -511,7 +515,9 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
         if ((uint32_t)s < nk) issue(s);
 
     for (uint32_t t = 0; t < nk; t++) {
-        wait_vmcnt<0>();   // two stages: everything issued so far is this stage
+        // stage t has landed once at most the next stage's loads are in flight
+        if (STAGES == 3 && t + 1 < nk) wait_vmcnt<G::MIN_LOADS>();
+        else wait_vmcnt<0>();
         __syncthreads();
         if (t + STAGES - 1 < nk) issue(t + STAGES - 1);
 
@@ -723,6 +729,7 @@ T0_W4_DECODE_NORM(4)
 T0_W4_PREFILL(256, 128, 2, 2, 2)
 T0_W4_PREFILL(256, 128, 4, 2, 2)
 T0_W4_PREFILL(128, 128, 2, 2, 2)
+T0_W4_PREFILL(128, 256, 2, 4, 3)
 
 extern "C" __global__ void __launch_bounds__(256) t0k_w4a16_rowsum(const t0_w4a16_params p) { t0::w4_rowsum(p); }
 extern "C" __global__ void __launch_bounds__(256) t0k_w4a16_generic(const t0_w4a16_params p) { t0::w4_generic(p); }
