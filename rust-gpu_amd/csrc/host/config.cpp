@@ -33,7 +33,7 @@ const std::vector<GemmInstance>& gemm_instances() {
     static const std::vector<GemmInstance> v = {
         {256, 256, 64, 2, 2, 2}, {256, 256, 64, 2, 4, 2}, {256, 256, 64, 4, 2, 2}, {256, 256, 32, 2, 2, 4},
         {256, 256, 32, 2, 4, 4}, {256, 128, 64, 2, 2, 3}, {128, 256, 64, 2, 2, 3},
-        {128, 128, 64, 2, 2, 4}, {128, 128, 32, 2, 2, 4}, {128, 64, 64, 2, 2, 4},  {64, 128, 64, 2, 2, 4},
+        {128, 128, 64, 2, 2, 4}, {128, 128, 32, 2, 2, 4}, {128, 64, 64, 2, 2, 4},  {64, 128, 64, 2, 2, 4}, {64, 64, 64, 2, 2, 4},
         {64, 64, 64, 1, 1, 4},   {32, 64, 64, 1, 1, 6},   {32, 128, 64, 1, 2, 4},
         {32, 64, 16, 1, 1, 4},   {32, 64, 32, 1, 1, 4},   {32, 128, 16, 1, 1, 4},
         {64, 64, 16, 1, 1, 4},   {64, 64, 32, 1, 1, 4},   {128, 64, 16, 2, 1, 4},
@@ -165,11 +165,12 @@ struct TileCost {
     double a_us, b_us;
 };
 constexpr TileCost kTileCost[] = {
-    {256, 256, 64, 8, 18.66, 19.05}, {256, 128, 64, 4, 10.24, 14.62}, {128, 256, 64, 4, 11.08, 14.85},
-    {128, 128, 64, 4, 5.09, 8.92},   {128, 64, 64, 4, 3.34, 6.50},    {64, 128, 64, 4, 3.38, 6.44},
-    {64, 64, 64, 1, 3.11, 11.02},    {32, 128, 64, 2, 5.27, 12.23},   {32, 64, 64, 1, 2.94, 7.91},
+    {256, 256, 64, 8, 18.83, 19.04}, {64, 64, 64, 4, 2.36, 6.23}, {256, 128, 64, 4, 10.32, 14.60},
+    {128, 256, 64, 4, 11.13, 14.85}, {128, 128, 64, 4, 5.09, 8.92}, {128, 64, 64, 4, 3.33, 6.50},
+    {64, 128, 64, 4, 3.35, 6.44}, {64, 64, 64, 1, 3.06, 11.04}, {32, 128, 64, 2, 5.22, 12.25},
+    {32, 64, 64, 1, 2.87, 7.93},
 };
-constexpr double kDisc = 0.888, kFixUs = 2.075, kFixUsPerMB = 0.427;
+constexpr double kDisc = 0.886, kFixUs = 2.254, kFixUsPerMB = 0.422;
 
 std::vector<Candidate> rank_candidates(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype,
                                        bool allow_fixup) {
