@@ -153,24 +153,32 @@ static uint32_t est_vgprs(const GemmInstance& g) {
     return fm * fn * 16 + (fm + fn) * 8 + 48;
 }
 
-// Per-tile cost, calibrated on MI355X: NN, bf16 out, M = 32..4096,
-// N = 1024..14336, K = 1024..11008, every tile below at split 1..8.  With a
-// full round of workgroups resident, one workgroup of the tile over k_len
-// takes a + b * k_len / 1000 us; a partly filled last round costs
-// DISC + (1 - DISC) * fill of a round; split-K adds FIX us plus FIX_MB us per
-// MB of partial planes.  Least squares on log time: median error 8 %, and the
-// pick is within 10 % of the measured best on every calibration shape.
+// Per-tile cost, calibrated on MI355X with every tile below at split 1..8
+// on 17 LLM shapes (NN, bf16 out, M = 32..4096, N = 1024..14336,
+// K = 1024..11008), B rotated through more copies than the 256 MB MALL holds
+// (a weight operand read cold from HBM, as in inference).  Predicted time:
+//   per workgroup  a + b * k_len / 1000 us while a round of workgroups
+//                  (CUs x workgroups per CU) is resident; a partly filled
+//                  last round costs DISC + (1 - DISC) * fill of a round;
+//   co-resident workgroups (2+ per CU) run at most 1/CO_RESIDENT as fast,
+//                  so ceil(workgroups / CUs) of them queue on one CU;
+//   memory         no faster than A + B + C over HBM_TBS, nor the operand
+//                  re-reads (A once per column tile, B once per row tile)
+//                  over L2_TBS;
+//   split-K        + FIX us + FIX_MB us per MB of partial planes.
+// Least squares on log time: median error 7 %; the pick is the measured best
+// on 10 of the 17 shapes and within 17 % on all.
 struct TileCost {
     uint32_t bm, bn, bk, nw;
     double a_us, b_us;
 };
 constexpr TileCost kTileCost[] = {
-    {256, 256, 64, 8, 18.83, 19.04}, {64, 64, 64, 4, 2.36, 6.23}, {256, 128, 64, 4, 10.32, 14.60},
-    {128, 256, 64, 4, 11.13, 14.85}, {128, 128, 64, 4, 5.09, 8.92}, {128, 64, 64, 4, 3.33, 6.50},
-    {64, 128, 64, 4, 3.35, 6.44}, {64, 64, 64, 1, 3.06, 11.04}, {32, 128, 64, 2, 5.22, 12.25},
-    {32, 64, 64, 1, 2.87, 7.93},
+    {256, 256, 64, 8, 16.86, 19.07}, {256, 128, 64, 4, 10.01, 14.05}, {128, 256, 64, 4, 10.37, 14.44},
+    {128, 128, 64, 4, 4.79, 8.88}, {128, 64, 64, 4, 3.58, 6.47}, {64, 128, 64, 4, 3.19, 6.59},
+    {64, 64, 64, 1, 2.18, 9.54}, {32, 128, 64, 2, 4.66, 10.35}, {32, 64, 64, 1, 2.13, 6.80},
 };
-constexpr double kDisc = 0.886, kFixUs = 2.254, kFixUsPerMB = 0.422;
+constexpr double kDisc = 0.977, kFixUs = 2.282, kFixUsPerMB = 0.439;
+constexpr double kHbmTBs = 3.429, kL2TBs = 13.841, kCoResident = 0.618;
 
 std::vector<Candidate> rank_candidates(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype,
                                        bool allow_fixup) {
@@ -189,7 +197,12 @@ std::vector<Candidate> rank_candidates(uint32_t m, uint32_t n, uint32_t k, uint3
             const double wgs = tiles * sk;
             const double full = std::floor(wgs / slots), fill = wgs / slots - full;
             const double rounds = full + (fill > 0 ? kDisc + (1 - kDisc) * fill : 0.0);
-            double t = rounds * (tc.a_us + tc.b_us * (k / (double)sk) / 1000.0);
+            const double t_wg = tc.a_us + tc.b_us * (k / (double)sk) / 1000.0;
+            double t = rounds * t_wg;
+            if (slots > hw::CUS) t = std::max(t, std::ceil(wgs / hw::CUS) * t_wg * kCoResident);
+            const double hbm = (double)k * n * 2 + (double)m * k * 2 + (double)m * n * 2;
+            const double l2 = (double)m * k * 2 * std::ceil((double)n / g->bn) + (double)n * k * 2 * std::ceil((double)m / g->bm);
+            t = std::max({t, hbm / (kHbmTBs * 1e6), l2 / (kL2TBs * 1e6)});
             if (sk > 1) t += kFixUs + kFixUsPerMB * wgs * g->bm * g->bn * 4 / 1e6;
             t0_gemm_config c = mk(g->bm, g->bn, g->bk, g->threads(), true, true, 1, false);
             c.split_k = sk > 1 ? sk : 0;

@@ -144,6 +144,25 @@ def test_torch_fixture_second_gemm(rt, dev, golden_dir):
     check_close(got_nn, ref, tolerance(f32(s), f32(wd), 512), "y nn")
 
 
+# ------------------------------------------------- instances beyond presets --
+
+@pytest.mark.parametrize("m,n,k,split", [(64, 4096, 1024, 4), (130, 200, 328, 1), (256, 192, 512, 2), (1, 64, 64, 1)])
+def test_64x64_four_wave_tile(rt, dev, m, n, k, split):
+    """The 64x64 tile on four waves (two workgroups per CU), reached by an
+    explicit config (tile 64x64x64, 256 threads): NN and NT, f32 and bf16
+    out, ragged M / N / K and in-kernel split-K."""
+    rng = np.random.default_rng(m + n + k)
+    a = bf16(rng.uniform(-1, 1, (m, k)))
+    b = bf16(rng.uniform(-1, 1, (k, n)))
+    ref = orc.gemm_nn(a, b)
+    tol = tolerance(f32(a), f32(b), k)
+    base = t0.GemmConfig.tile_64x64_k64().copy(wg_size=256, split_k=split if split > 1 else 0)
+    for layout, bb in ((t0.NN, b), (t0.NT, b.T.copy())):
+        for od in (t0.OUT_F32, t0.OUT_BF16):
+            got = run_gemm(rt, dev, a, bb, m, n, k, layout, od, cfg=base.copy(transpose=layout, out_dtype=od))
+            check_close(got, ref, tol, f"64x64 w4 {m}x{n}x{k} split {split} layout={layout} out={od}")
+
+
 # ----------------------------------------------------------------- bounds --
 
 @pytest.mark.parametrize("m,n,k", [(33, 31, 40), (1, 1, 8), (255, 257, 264), (100, 200, 72), (300, 130, 1000)])
