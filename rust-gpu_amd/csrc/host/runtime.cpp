@@ -1141,7 +1141,7 @@ int t0_w4a16_gemm(t0_runtime* rt, const t0_w4a16_desc* d) {
         p.semaphores = rt->sem;
     }
     if (pl.kind == 2) {
-        // X[g][m] = -144 * group row sums of A (plus 1 KiB tail the DMA may touch)
+        // R[g][m] = group row sums of A (plus 1 KiB tail the DMA may touch)
         const uint32_t G = p.K / 128;
         r = ensure_ws(rt, (size_t)G * p.M * 4 + 2048);
         if (r) return r;
