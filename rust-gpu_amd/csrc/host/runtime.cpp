@@ -1258,6 +1258,7 @@ int stage_cvt_t(t0_runtime* rt, uint64_t src, uint32_t ld_src, uint32_t m, uint3
     memset(&p, 0, sizeof p);
     p.src = (const void*)src; p.dst = (void*)dst;
     p.m = m; p.n = n; p.ld_src = ld_src; p.ld_dst = ld_dst; p.rows_pad = rows_pad;
+    p.flags = (aligned16(src) && ld_src % 4 == 0) ? T0_AUX_SRC_VEC4 : 0;
     const uint64_t tiles = (uint64_t)((ld_dst + 63) / 64) * ((rows_pad + 63) / 64);
     return launch(rt, f, (uint32_t)tiles, 1, 1, 256, p);
 }

@@ -116,17 +116,33 @@ __device__ __forceinline__ void cvt_pad_bf16(const t0_aux_params& p) {
 //             = 0               for m <= r < ld_dst or n <= c < rows_pad
 // src f32 [m][ld_src]; dst bf16 [rows_pad][ld_dst], ld_dst a multiple of 8.
 // A 256-lane workgroup moves one 64 x 64 tile through LDS: coalesced f32 row
-// reads, then 16-byte bf16 row writes of the transposed tile.
+// reads (16 bytes per lane with T0_AUX_SRC_VEC4: 16-byte aligned source and
+// a row stride of 4k floats), then 16-byte bf16 row writes of the transposed
+// tile.
 __device__ __forceinline__ void cvt_t_bf16(const t0_aux_params& p) {
     __shared__ float tile[64][65];
     const uint32_t tiles_c = (p.rows_pad + 63) / 64;             // along src columns
     const uint32_t r0 = (blockIdx.x / tiles_c) * 64, c0 = (blockIdx.x % tiles_c) * 64;
     const uint32_t t = threadIdx.x;
     const float* src = (const float*)p.src;
+    const bool vec = p.flags & T0_AUX_SRC_VEC4;
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const uint32_t idx = t + 256 * i, r = idx / 64, c = idx % 64;
-        tile[r][c] = (r0 + r < p.m && c0 + c < p.n) ? src[(size_t)(r0 + r) * p.ld_src + c0 + c] : 0.0f;
+    for (int i = 0; i < 4; i++) {
+        const uint32_t idx = t + 256 * i, r = idx / 16, c = (idx % 16) * 4;
+        const uint32_t gr = r0 + r, gc = c0 + c;
+        f32x4_t v = {0.f, 0.f, 0.f, 0.f};
+        if (gr < p.m) {
+            const float* row = src + (size_t)gr * p.ld_src;
+            if (vec && gc + 4 <= p.n) {
+                v = *(const f32x4_t*)(row + gc);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (gc + e < p.n) v[e] = row[gc + e];
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) tile[r][c + e] = v[e];
     }
     __syncthreads();
 #pragma unroll
