@@ -67,6 +67,10 @@ struct t0_runtime {
     size_t stage_bytes = 0;
     uint32_t* sem = nullptr;
     size_t sem_count = 0;
+    // Held for the host side of every call that uses ws / stage / sem, so
+    // that threads sharing the runtime never resize a buffer another call
+    // has just put into its kernel arguments (recursive: calls nest).
+    std::recursive_mutex call_mu;
     uint32_t slot = 0;
     std::string arch;
     int cu_count = 0, clock_khz = 0;
@@ -754,6 +758,7 @@ int t0_gemm_select(t0_runtime* rt, const t0_gemm_desc* d, t0_gemm_config* out) {
 
 int t0_gemm(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm_desc* d) {
     if (!rt || !d) return fail(T0_ERR_INVALID, "null argument");
+    std::lock_guard<std::recursive_mutex> call_lock(rt->call_mu);
     if (!d->m || !d->n || !d->k) return fail(T0_ERR_INVALID, "empty GEMM %ux%ux%u", d->m, d->n, d->k);
     if (d->transpose > T0_NN || d->out_dtype > T0_OUT_BF16) return fail(T0_ERR_INVALID, "bad layout / out_dtype");
     t0_gemm_config c;
@@ -1111,6 +1116,7 @@ int t0_w4a16_plan(t0_runtime* rt, const t0_w4a16_desc* d, char* kernel, size_t l
 
 int t0_w4a16_gemm(t0_runtime* rt, const t0_w4a16_desc* d) {
     if (!rt || !d || !d->a || !d->qweight || !d->scales || !d->c) return fail(T0_ERR_INVALID, "null argument");
+    std::lock_guard<std::recursive_mutex> call_lock(rt->call_mu);
     W4Plan pl;
     int r = w4_plan(rt, d, pl);
     if (r) return r;
@@ -1299,6 +1305,7 @@ extern "C" {
 int t0_bf16_matmul(t0_runtime* rt, uint64_t x, uint64_t w, uint64_t y, uint32_t m, uint32_t k, uint32_t n) {
     int r = matmul_args(rt, x, w, y, m, k, n);
     if (r) return r;
+    std::lock_guard<std::recursive_mutex> call_lock(rt->call_mu);
     const uint32_t k8 = round8(k), n8 = round8(n);
     const size_t a_bytes = align256((size_t)m * k8 * 2), b_bytes = align256((size_t)k8 * n8 * 2);
     r = ensure_stage(rt, a_bytes + b_bytes);
@@ -1313,6 +1320,7 @@ int t0_bf16_matmul_backward_data(t0_runtime* rt, uint64_t dy, uint64_t w, uint64
                                  uint32_t n) {
     int r = matmul_args(rt, dy, w, dx, m, k, n);
     if (r) return r;
+    std::lock_guard<std::recursive_mutex> call_lock(rt->call_mu);
     const uint32_t n8 = round8(n);
     const size_t a_bytes = align256((size_t)m * n8 * 2), b_bytes = align256((size_t)k * n8 * 2);
     r = ensure_stage(rt, a_bytes + b_bytes);
@@ -1327,6 +1335,7 @@ int t0_bf16_matmul_backward_weight(t0_runtime* rt, uint64_t x, uint64_t dy, uint
                                    uint32_t n) {
     int r = matmul_args(rt, x, dy, dw, m, k, n);
     if (r) return r;
+    std::lock_guard<std::recursive_mutex> call_lock(rt->call_mu);
     const uint32_t m8 = round8(m), n8 = round8(n);
     const size_t a_bytes = align256((size_t)k * m8 * 2), b_bytes = align256((size_t)m8 * n8 * 2);
     r = ensure_stage(rt, a_bytes + b_bytes);
@@ -1341,6 +1350,7 @@ int t0_bf16_matmul_with_wt_bf16(t0_runtime* rt, uint64_t x, uint64_t wt, uint64_
                                 uint32_t n) {
     int r = matmul_args(rt, x, wt, y, m, k, n);
     if (r) return r;
+    std::lock_guard<std::recursive_mutex> call_lock(rt->call_mu);
     const uint32_t k8 = round8(k);
     const size_t a_bytes = align256((size_t)m * k8 * 2);
     r = ensure_stage(rt, a_bytes);
@@ -1411,6 +1421,7 @@ int t0_rmsnorm(t0_runtime* rt, uint64_t residual, uint64_t hidden, uint64_t gamm
 int t0_rmsnorm_w4a16(t0_runtime* rt, const t0_w4a16_desc* d, const t0_rmsnorm_desc* nd) {
     if (!rt || !d || !nd || !nd->residual || !nd->gamma || !d->qweight || !d->scales || !d->c)
         return fail(T0_ERR_INVALID, "null argument");
+    std::lock_guard<std::recursive_mutex> call_lock(rt->call_mu);
     if (!d->m || !d->k) return fail(T0_ERR_INVALID, "empty problem");
     int r = set_dev(rt);
     if (r) return r;
@@ -1468,6 +1479,7 @@ int t0_rmsnorm_matmul(t0_runtime* rt, uint64_t residual, uint64_t hidden, uint64
                       uint64_t x2_out, uint32_t m, uint32_t k, uint32_t n, float eps) {
     int r = matmul_args(rt, residual, w, y, m, k, n);
     if (r) return r;
+    std::lock_guard<std::recursive_mutex> call_lock(rt->call_mu);
     if (!gamma) return fail(T0_ERR_INVALID, "null gamma");
     const uint32_t k8 = round8(k), n8 = round8(n);
     const size_t a_bytes = align256((size_t)m * k8 * 2), b_bytes = align256((size_t)k8 * n8 * 2);

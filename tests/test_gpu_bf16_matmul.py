@@ -149,3 +149,43 @@ def test_shape_errors(rt):
     with pytest.raises(t0.T0Error, match="empty matmul"):     # the C ABI rejects m = 0 itself
         t0._check(t0.lib().t0_bf16_matmul(rt.h, bx.gpu_addr(), bw.gpu_addr(), bw.gpu_addr(), 0, 8, 4))
     bx.free(), bw.free()
+
+
+def test_threads_share_one_runtime():
+    """Four host threads drive one runtime at once: the staging matmul and the
+    in-kernel split-K GEMM, with sizes that grow the runtime's staging buffer
+    and split-K workspace while the other threads' calls are in flight.  Every
+    result matches the oracle."""
+    import threading
+    r = t0.GpuRuntime(0)
+    errors = []
+
+    def worker(tid):
+        try:
+            rng = np.random.default_rng(100 + tid)
+            for step in range(4):
+                m, k, n = 64 * (step + 1) + tid, 256 * (step + 1), 96 * (step + 1) + 8 * tid
+                x, w = _rand(rng, (m, k)), _rand(rng, (k, n), 0.5)
+                bx, bw = r.upload(x), r.upload(w)
+                y = bm.matmul(r, bx, bw, (m, k), (k, n))
+                check_close(_down(r, y, (m, n)), orc.bf16_matmul(x, w), _tol(x, w, k), f"t{tid} matmul {m}x{k}x{n}")
+                a16, b16 = bf16(x), bf16(w)
+                da, db, dc = r.upload(a16), r.upload(b16), r.alloc(m * n * 2)
+                cfg = t0.GemmConfig.tile_128x128_k64().copy(split_k=4, transpose=t0.NN, out_dtype=t0.OUT_BF16)
+                r.gemm(da.gpu_addr(), db.gpu_addr(), dc.gpu_addr(), m, n, k, transpose=t0.NN, out_dtype=t0.OUT_BF16,
+                       cfg=cfg)
+                r.wait_idle()
+                got = f32(dc.read(np.uint16, m * n).reshape(m, n))
+                check_close(got, orc.gemm_nn(a16, b16), tolerance(f32(a16), f32(b16), k), f"t{tid} split-K {m}x{n}x{k}")
+                for b in (bx, bw, da, db, dc):
+                    b.free()
+        except Exception as e:          # reported by the main thread
+            errors.append(f"thread {tid}: {e!r}")
+
+    ts = [threading.Thread(target=worker, args=(i,)) for i in range(4)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    r.close()
+    assert not errors, errors
