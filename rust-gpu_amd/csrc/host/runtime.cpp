@@ -59,6 +59,7 @@ struct t0_runtime {
     std::mutex mu;
     std::map<std::string, t0_kernel*> cache;
     std::map<std::string, hipFunction_t> fns;
+    std::mutex fn_mu;               // guards fns
     std::atomic<bool> poisoned{false};
     std::map<size_t, std::vector<t0_buffer*>> pool;
     void* ws = nullptr;
@@ -71,7 +72,7 @@ struct t0_runtime {
     // that threads sharing the runtime never resize a buffer another call
     // has just put into its kernel arguments (recursive: calls nest).
     std::recursive_mutex call_mu;
-    uint32_t slot = 0;
+    std::atomic<uint32_t> slot{0};  // t0_dispatch_async's completion slots
     std::string arch;
     int cu_count = 0, clock_khz = 0;
 };
@@ -90,6 +91,7 @@ int set_dev(t0_runtime* rt) {
 }
 
 int get_fn(t0_runtime* rt, const std::string& sym, hipFunction_t* out) {
+    std::lock_guard<std::mutex> g(rt->fn_mu);
     auto it = rt->fns.find(sym);
     if (it != rt->fns.end()) { *out = it->second; return T0_OK; }
     hipFunction_t f;
@@ -535,7 +537,7 @@ int t0_dispatch(t0_runtime* rt, const t0_kernel* k, const uint32_t grid[3], cons
 int t0_dispatch_async(t0_runtime* rt, const t0_kernel* k, const uint32_t grid[3], const void* ka, size_t len) {
     int r = dispatch_impl(rt, k, grid, ka, len);
     if (r) return r;
-    return (int)(rt->slot++ % 256);
+    return (int)(rt->slot.fetch_add(1) % 256);
 }
 
 int t0_wait_idle(t0_runtime* rt) {
