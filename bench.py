@@ -3,13 +3,13 @@
 
 One JSON line on stdout.  The headline ``value`` is the bf16 GEMM
 M = N = K = 4096 (NN, N(0,1) inputs rounded to bf16, fp32 accumulate, bf16
-output), in TFLOP/s: whole-job throughput of ``--steps``
+output; the compute-bound headline shape), in TFLOP/s: whole-job throughput of ``--steps``
 back-to-back GEMMs with inputs resident in HBM, timed with HIP events on the
 library's stream.  ``roofline`` relates the GEMM kernel's average launch
 duration to MI355X's dense bf16 MFMA peak (2516.6 TFLOP/s); ``cpu_baseline``
 times the reference's CPU matmul (restated in oracle/, single thread) on a
-row slice of the same workload.  ``extras`` carries the other BASELINE
-configs: skinny bf16 GEMM (HBM), W4A16 decode (HBM, the metric's second
+row slice of the same workload.  ``extras`` carries the other workloads
+of the path: skinny bf16 GEMM (HBM), W4A16 decode (HBM, the metric's second
 half), W4A16 prefill (MFMA), each with its own roofline, and the Ignis
 f32 matmul forward / backward at 4096^3 (staging conversions + GEMM); the HBM-bound
 shapes rotate 12 weight copies (> 256 MB) so the Infinity Cache cannot
@@ -335,7 +335,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU; --gpus must be 1 (the path would shard by N or K "
-              "across GPUs, see DESIGN.md)", file=sys.stderr)
+              "across GPUs)", file=sys.stderr)
         sys.exit(2)
 
     global USE_GRAPHS

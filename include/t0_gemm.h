@@ -3,8 +3,8 @@
  *
  * Drop-in boundary for the reference crate t0-gpu ("T0-GPU"): every entry
  * point below replaces one Rust item on the reference's GEMM path, cited as
- * file:line into the reference tree.  Rust callers bind these through the
- * extern "C" block shown in INTEGRATION.md.
+ * file:line into the reference tree.  Rust callers bind these through an
+ * extern "C" block with the same signatures.
  *
  * Conventions
  *  - Every function returns T0_OK (0) or a negative t0_status; the message of

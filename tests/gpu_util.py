@@ -1,5 +1,5 @@
 """Helpers for the GPU parity tests: data generation through the oracle's
-bf16 rounding, device round trips, and the BASELINE tolerance
+bf16 rounding, device round trips, and the acceptance tolerance
 max|err| <= 1e-2 * sqrt(K) * max|a| * max|b| (relative Frobenius error is
 reported alongside)."""
 import numpy as np

@@ -1,7 +1,7 @@
 """Ignis bf16 matmul path (src/ignis/ops/bf16_matmul.rs) on the GPU: f32
 operands converted, padded and transposed by the library's kernels, checked
 against the oracle (bf16 RNE of both operands, then the reference CPU
-product) -- bit-exact on integer inputs, within the BASELINE tolerance
+product) -- bit-exact on integer inputs, within the acceptance tolerance
 1e-2 * sqrt(K) * max|a| * max|b| on random inputs."""
 import numpy as np
 import pytest

@@ -340,7 +340,7 @@ def _sampled_rows(m, count=16):
 
 
 def test_headline_4096_nn_bf16(rt, dev):
-    """4096^3 NN, N(0,1) bf16 inputs, bf16 output; sampled
+    """The headline shape: 4096^3 NN, N(0,1) bf16 inputs, bf16 output; sampled
     rows against the oracle (full oracle is 137 GFLOP), plus the chosen
     kernel against a second kernel on the whole matrix."""
     m = n = k = 4096
@@ -357,7 +357,7 @@ def test_headline_4096_nn_bf16(rt, dev):
 
 
 def test_skinny_128x4096x4096(rt, dev):
-    """M=128, N=K=4096, N(0,0.02) inputs, bf16 out."""
+    """The skinny shape: M=128, N=K=4096, N(0,0.02) inputs, bf16 out."""
     m, n, k = 128, 4096, 4096
     rng = np.random.default_rng(43)
     a = bf16(rng.normal(0, 0.02, (m, k)))

@@ -4,7 +4,7 @@ by raw dispatch, the row RMSNorm, and the Ignis fused ops
 (src/ignis/ops/fused_rmsnorm_gemm.rs) on an INT4 weight (the decode kernel
 with the norm fused in for one row) and on a dense f32 weight.  Checked
 against the oracle: bit-exact where the arithmetic is exact (x2, integer
-closed forms), else within the BASELINE tolerance
+closed forms), else within the acceptance tolerance
 1e-2 * sqrt(K) * max|a| * max|w| or the reference tests' own 1e-4."""
 import struct
 

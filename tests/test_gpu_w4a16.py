@@ -126,7 +126,7 @@ def test_w4a16_decode_f32_scales(rt, dev):
 
 
 def test_w4a16_decode_headline(rt, dev):
-    """A[16,4096] ~ N(0,1), W[4096,11008] int4, g=128,
+    """The decode headline: A[16,4096] ~ N(0,1), W[4096,11008] int4, g=128,
     bf16 scales ~U(0.005,0.02), z = 8; checked on a 1376-column block and
     with an integer closed form over the whole matrix."""
     rng = np.random.default_rng(44)
@@ -216,7 +216,7 @@ def test_w4a16_prefill_exact_integers(rt, dev, per_group_zeros):
 
 
 def test_w4a16_prefill_headline_rows(rt, dev):
-    """4096x4096x14336, per-group zero points; sampled rows."""
+    """The prefill shape: 4096x4096x14336, per-group zero points; sampled rows."""
     rng = np.random.default_rng(45)
     m, n, k, gs = 4096, 14336, 4096, 128
     qw, s, zw = make_w4(rng, n, k, gs, per_group_zeros=True)
