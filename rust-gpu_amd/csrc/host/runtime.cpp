@@ -1084,7 +1084,7 @@ static int w4_plan(t0_runtime* rt, const t0_w4a16_desc* d, W4Plan& pl) {
         pl.bn = 16 * tiles;
         return T0_OK;
     }
-    if (fast && M > 64 && N % 8 == 0 && !d->scales_f32) {
+    if (fast && M > 64 && N % 8 == 0 && (!d->scales_f32 || d->scales % 16 == 0)) {
         const bool big = M >= 1024;
         pl.bm = 128;
         pl.bn = big ? 256 : 128;
@@ -1149,17 +1149,25 @@ int t0_w4a16_gemm(t0_runtime* rt, const t0_w4a16_desc* d) {
         p.semaphores = rt->sem;
     }
     if (pl.kind == 2) {
-        // R[g][m] = group row sums of A (plus 1 KiB tail the DMA may touch)
+        // workspace: R[g][m] = group row sums of A; bf16 scales widened to
+        // f32 [G][N] (the prefill reads f32 scales); a 2 KiB tail the
+        // row-sum DMA may touch
         const uint32_t G = p.K / 128;
-        r = ensure_ws(rt, (size_t)G * p.M * 4 + 2048);
+        const size_t r_bytes = ((size_t)G * p.M * 4 + 255) & ~(size_t)255;
+        const bool widen = !d->scales_f32;
+        r = ensure_ws(rt, r_bytes + (widen ? (size_t)G * p.N * 4 : 0) + 2048);
         if (r) return r;
         p.workspace = (float*)rt->ws;
+        if (widen) p.scales_f32 = (float*)((uint8_t*)rt->ws + r_bytes);
         hipFunction_t fr;
         r = get_fn(rt, "t0k_w4a16_rowsum", &fr);
         if (r) return r;
-        const uint32_t waves = p.M * ((G + 7) / 8);
-        r = launch(rt, fr, (waves + 3) / 4, 1, 1, 256, p);
+        const uint32_t sum_blocks = (p.M * ((G + 7) / 8) + 3) / 4;
+        const uint32_t widen_blocks = widen ? (uint32_t)(((uint64_t)G * p.N / 4 + 255) / 256) : 0;
+        r = launch(rt, fr, sum_blocks + widen_blocks, 1, 1, 256, p);
         if (r) return r;
+        if (widen) p.scales = p.scales_f32;
+        p.flags |= T0_W4_SCALE_F32;
     }
     r = get_fn(rt, pl.sym, &f);
     if (r) return r;

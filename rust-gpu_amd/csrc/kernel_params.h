@@ -76,6 +76,7 @@ typedef struct t0_w4a16_params {
     float* norm_x2;           // [K] or NULL: x2, written by workgroup 0
     float norm_eps;
     uint32_t pad2_;
+    float* scales_f32;        // prefill pre-pass: bf16 scales widened to f32 [G][N]
 } t0_w4a16_params;
 
 // The reference's fused residual add + RMSNorm + row projection kernel,

@@ -382,7 +382,7 @@ __device__ __forceinline__ void w4_decode(const t0_w4a16_params& p) {
 //   Stage (LDS, filled by buffer_load ... lds):
 //     A  [BM][128] bf16, 16-B chunks swizzled by row         BM*256 B
 //     W  [BN][16 words] packed nibbles, chunk-swizzled         BN*64 B
-//     S  [BN] bf16 scales of this group                        BN*2 B (padded to 1 KB slot)
+//     S  [BN] f32 scales of this group                         BN*4 B (1 KB slot)
 //     R  [BM] f32: sum_k a[m][k] over this group                BM*4 B
 //   MFMA step kk (0..7) takes, in lane half h, the 8 k of word h*8 + kk, so a
 //   lane reads its W column as two 16-B LDS loads per group.
@@ -394,7 +394,8 @@ __device__ __forceinline__ void w4_decode(const t0_w4a16_params& p) {
 //       times (an exact bf16 integer), the other 13 k zero;
 //   then acc += s_n * T, one FMA per output per group.
 // Requires: group_size == 128, K % 128 == 0, lda % 8 == 0, N % 8 == 0,
-//           R precomputed by w4_rowsum into workspace [G][M].
+//           R precomputed by w4_rowsum into workspace [G][M], f32 scales
+//           (bf16 scales are widened by the same pre-pass).
 // ---------------------------------------------------------------------------
 template <int CH>
 T0_DEV uint32_t swz16(uint32_t r) { return r & (CH - 1) & 15; }
@@ -405,7 +406,7 @@ struct W4Cfg {
     static constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
     static constexpr int A_BYTES = BM * 256;
     static constexpr int W_BYTES = BN * 64;
-    // The scale DMA writes all 64 lanes x 16 B (1 KB, lanes past BN*2 bytes
+    // The scale DMA writes all 64 lanes x 16 B (1 KB, lanes past BN*4 bytes
     // write zeros), the zero-point DMA 64 x 4 B: separate slots.
     static constexpr int S_BYTES = 2048;                 // scales [0, 1024), zero-point words [1024, 1280)
     static constexpr int Z_OFF = 1024;
@@ -417,7 +418,7 @@ struct W4Cfg {
     static constexpr int SMEM = (STAGE * STAGES > NW * 32 * EPI_LD * 4) ? STAGE * STAGES : NW * 32 * EPI_LD * 4;
     static_assert(A_LOADS >= 1 && A_LOADS * 1024 * NW == A_BYTES, "A split");
     static_assert(W_LOADS >= 1 && W_LOADS * 1024 * NW == W_BYTES, "W split");
-    static_assert(BN * 2 <= Z_OFF && BM * 4 <= 1024 * 2, "S/Z/X slots");
+    static_assert(BN * 4 <= Z_OFF && BM * 4 <= 1024 * 2, "S/Z/X slots");
     static_assert(NW >= 3, "S, Z and X DMAs go out from three different waves");
     static_assert(SMEM <= 160 * 1024, "LDS");
     static_assert(STAGES == 2 || STAGES == 3, "stage waits below");
@@ -445,7 +446,7 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
     const uint32_t lda = p.lda;
     const uint8_t* A0 = (const uint8_t*)p.A + (size_t)m0 * lda * 2;
     const uint8_t* W0 = (const uint8_t*)p.qweight + (size_t)n0 * (K / 2);
-    const uint8_t* S0 = (const uint8_t*)p.scales + (size_t)n0 * 2;
+    const uint8_t* S0 = (const uint8_t*)p.scales + (size_t)n0 * 4;   // f32
     const float* X = p.workspace;   // [G][M]
 
     // per-lane DMA offsets
@@ -464,7 +465,7 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
         const uint32_t lc = c ^ (((r >> 1) ^ (r >> 3)) & 3);
         w_off[j] = (n0 + r < N) ? r * (K / 2) + lc * 16 : OOB_OFFSET;
     }
-    const uint32_t s_off = (lane * 16 < BN * 2 && n0 + lane * 8 < N) ? lane * 16 : OOB_OFFSET;
+    const uint32_t s_off = (lane * 16 < BN * 4 && n0 + lane * 4 < N) ? lane * 16 : OOB_OFFSET;
     const uint32_t z_off = (lane < BN / 8 && n0 + lane * 8 < N) ? lane * 4 : OOB_OFFSET;   // zero-point word per lane
     const uint32_t x_off = (lane * 16 < BM * 4 && m0 + lane * 4 < M) ? lane * 16 : OOB_OFFSET;
     const uint32_t x_off2 = (1024 + lane * 16 < BM * 4 && m0 + 256 + lane * 4 < M) ? 1024 + lane * 16 : OOB_OFFSET;
@@ -481,7 +482,7 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
         for (int j = 0; j < G::W_LOADS; j++)
             dma_x4(rw, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + (wave * G::W_LOADS + j) * 1024), w_off[j]);
         if (wave == 0) {
-            __amdgpu_buffer_rsrc_t rs = make_rsrc(S0 + (size_t)t * N * 2);
+            __amdgpu_buffer_rsrc_t rs = make_rsrc(S0 + (size_t)t * N * 4);
             dma_x4(rs, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + G::W_BYTES), s_off);
         } else if (wave == 1) {
             if (p.zeros) {
@@ -510,6 +511,27 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
     const uint32_t w_c0 = ((2 * h) ^ w_sw) * 16, w_c1 = ((2 * h + 1) ^ w_sw) * 16;
     const uint32_t bits4300 = __builtin_amdgcn_mov_dpp(0x43004300u, 0xE4, 0xF, 0xF, false);  // in a VGPR
 
+    // acc += s_n * T for the group whose products are in tmp; sv holds its
+    // scales for (j, q4) = columns wn*TN + j*32 + 8*q4 + 4*h .. +3
+    f32x16_t tmp[G::FM][G::FN];
+    f32x4_t sv[G::FN][4];
+    auto scale_add = [&]() {
+#pragma unroll
+        for (int j = 0; j < G::FN; j++)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; q4++)
+#pragma unroll
+                for (int i = 0; i < G::FM; i++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        acc[i][j][4 * q4 + r] = fmaf(sv[j][q4][r], tmp[i][j][4 * q4 + r], acc[i][j][4 * q4 + r]);
+    };
+    // With two waves per SIMD (waves w and w + 4), the barrier of every step
+    // starts both in the same phase, so one's MFMAs cannot hide the other's
+    // scale FMAs.  The second half of the waves therefore applies a group's
+    // scales at the start of the next step, under the first half's MFMAs.
+    const bool late = G::NW >= 8 && ((wave >> 2) & 1);
+
 #pragma unroll
     for (int s = 0; s < STAGES - 1; s++)
         if ((uint32_t)s < nk) issue(s);
@@ -520,16 +542,22 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
         else wait_vmcnt<0>();
         __syncthreads();
         if (t + STAGES - 1 < nk) issue(t + STAGES - 1);
+        if (late && t > 0) scale_add();
+        __builtin_amdgcn_sched_barrier(0);
 
         const LDS_AS uint8_t* st = (const LDS_AS uint8_t*)smem + (t % STAGES) * G::STAGE;
         const LDS_AS uint8_t* sa = st;
         const LDS_AS uint8_t* sw = st + G::A_BYTES;
-        const LDS_AS uint16_t* ss = (const LDS_AS uint16_t*)(st + G::A_BYTES + G::W_BYTES);
+        const LDS_AS float* ss = (const LDS_AS float*)(st + G::A_BYTES + G::W_BYTES);
         const LDS_AS uint32_t* sz = (const LDS_AS uint32_t*)(st + G::A_BYTES + G::W_BYTES + G::Z_OFF);
         const LDS_AS float* sx = (const LDS_AS float*)(st + G::A_BYTES + G::W_BYTES + G::S_BYTES);
 
         // this lane's W words, and the correction block's operands: B column
         // -(128 + z) in k 0..2 of lane half 0, A row R split hi/mid/lo likewise
+        bf16x8_t af[2][G::FM];
+#pragma unroll
+        for (int i = 0; i < G::FM; i++)
+            af[0][i] = *(const LDS_AS bf16x8_t*)(sa + a_row0 + i * 32 * 256 + ((h * 8) ^ a_sw) * 16);
         u32x4_t wlo[G::FN], whi[G::FN];
         bf16x8_t zcol[G::FN], rrow[G::FM];
 #pragma unroll
@@ -551,7 +579,6 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
             const uint32_t lo = __float_as_uint(r1 - __uint_as_float(mid)); // <= 8 significant bits: exact in bf16
             rrow[i] = __builtin_bit_cast(bf16x8_t, u32x4_t{(hi >> 16) | mid, lo >> 16, 0u, 0u});
         }
-        f32x16_t tmp[G::FM][G::FN];
 #pragma unroll
         for (int i = 0; i < G::FM; i++)
 #pragma unroll
@@ -559,39 +586,32 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
                 tmp[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(zcol[j], rrow[i], f32x16_t{}, 0, 0, 0);
 #pragma unroll
         for (int kk = 0; kk < 8; kk++) {
-            bf16x8_t af[G::FM], bw[G::FN];
+            const int cur = kk & 1;
+            if (kk + 1 < 8) {
 #pragma unroll
-            for (int i = 0; i < G::FM; i++) {
-                const uint32_t c = (h * 8 + kk) ^ a_sw;
-                af[i] = *(const LDS_AS bf16x8_t*)(sa + a_row0 + i * 32 * 256 + c * 16);
+                for (int i = 0; i < G::FM; i++) {
+                    const uint32_t c = (h * 8 + kk + 1) ^ a_sw;
+                    af[cur ^ 1][i] = *(const LDS_AS bf16x8_t*)(sa + a_row0 + i * 32 * 256 + c * 16);
+                }
             }
+            bf16x8_t bw[G::FN];
 #pragma unroll
             for (int j = 0; j < G::FN; j++) bw[j] = unpack8_128(kk < 4 ? wlo[j][kk] : whi[j][kk - 4], bits4300);
 #pragma unroll
             for (int i = 0; i < G::FM; i++)
 #pragma unroll
                 for (int j = 0; j < G::FN; j++)
-                    tmp[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[j], af[i], tmp[i][j], 0, 0, 0);
+                    tmp[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[j], af[cur][i], tmp[i][j], 0, 0, 0);
         }
-        // acc += s_n * T
+        // this group's scales (the buffer is refilled after the next barrier)
 #pragma unroll
-        for (int j = 0; j < G::FN; j++) {
+        for (int j = 0; j < G::FN; j++)
 #pragma unroll
-            for (int q4 = 0; q4 < 4; q4++) {
-                const uint32_t ncol = wn * G::TN + j * 32 + 8 * q4 + 4 * h;
-                const u32x2_t sv = *(const LDS_AS u32x2_t*)(ss + ncol);
-                const float s0 = __uint_as_float(sv[0] << 16), s1 = __uint_as_float(sv[0] & 0xFFFF0000u);
-                const float s2 = __uint_as_float(sv[1] << 16), s3 = __uint_as_float(sv[1] & 0xFFFF0000u);
-#pragma unroll
-                for (int i = 0; i < G::FM; i++) {
-                    acc[i][j][4 * q4 + 0] = fmaf(s0, tmp[i][j][4 * q4 + 0], acc[i][j][4 * q4 + 0]);
-                    acc[i][j][4 * q4 + 1] = fmaf(s1, tmp[i][j][4 * q4 + 1], acc[i][j][4 * q4 + 1]);
-                    acc[i][j][4 * q4 + 2] = fmaf(s2, tmp[i][j][4 * q4 + 2], acc[i][j][4 * q4 + 2]);
-                    acc[i][j][4 * q4 + 3] = fmaf(s3, tmp[i][j][4 * q4 + 3], acc[i][j][4 * q4 + 3]);
-                }
-            }
-        }
+            for (int q4 = 0; q4 < 4; q4++)
+                sv[j][q4] = *(const LDS_AS f32x4_t*)(ss + wn * G::TN + j * 32 + 8 * q4 + 4 * h);
+        if (!late) scale_add();
     }
+    if (late && nk) scale_add();
 
     // epilogue: stage 32-row blocks through LDS, store rows
     __syncthreads();
@@ -615,12 +635,25 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
     }
 }
 
-// R[g][m] = sum_{k in group g} a[m][k]   (prefill pre-pass, group 128)
+// Prefill pre-pass (group 128), 256 threads per block:
+//   R[g][m] = sum_{k in group g} a[m][k] into workspace [G][M];
+//   with bf16 scales, the blocks past the row sums widen them to f32 into
+//   p.scales_f32 [G][N] (four per thread).
 __device__ __forceinline__ void w4_rowsum(const t0_w4a16_params& p) {
+    const uint32_t G = p.K / 128;
+    const uint32_t sum_blocks = (p.M * ((G + 7) / 8) + 3) / 4;
+    if (blockIdx.x >= sum_blocks) {
+        const uint32_t q = (blockIdx.x - sum_blocks) * 256 + threadIdx.x;   // 4 scales
+        if (q < G * p.N / 4) {
+            const u32x2_t v = ((const u32x2_t*)p.scales)[q];
+            ((f32x4_t*)p.scales_f32)[q] = f32x4_t{__uint_as_float(v[0] << 16), __uint_as_float(v[0] & 0xFFFF0000u),
+                                                  __uint_as_float(v[1] << 16), __uint_as_float(v[1] & 0xFFFF0000u)};
+        }
+        return;
+    }
     // one wave per (m, 8 groups): lane covers 16 k of a group
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wid = blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
-    const uint32_t G = p.K / 128;
     const uint32_t m = wid / ((G + 7) / 8);
     const uint32_t g8 = wid % ((G + 7) / 8);
     if (m >= p.M) return;

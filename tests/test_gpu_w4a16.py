@@ -188,6 +188,23 @@ def test_w4a16_prefill(rt, dev, m, n):
     check_close(got, ref, w4_tol(a, qw, s, zw, 0, n, k, gs), f"prefill {m}x{n}")
 
 
+@pytest.mark.parametrize("m,n", [(300, 264), (1024, 256)])
+def test_w4a16_prefill_f32_scales(rt, dev, m, n):
+    """f32 scales reach the prefill kernel as given; bf16 scales are widened
+    to f32 by its pre-pass, so the same scale values give the same bits."""
+    rng = np.random.default_rng(3 * m + n)
+    k, gs = 512, 128
+    qw, s, zw = make_w4(rng, n, k, gs, per_group_zeros=True)
+    a = bf16(rng.standard_normal((m, k)))
+    plan, _ = rt.w4a16_plan(0, 0, 0, 0, 0, m, n, k, group_size=gs, scales_f32=True)
+    assert plan.startswith("t0k_w4a16_prefill"), plan
+    got32 = run_w4(rt, dev, a, qw, s, zw, m, n, k, gs, zc=0, out_f32=True, scales_f32=True)
+    got16 = run_w4(rt, dev, a, qw, s, zw, m, n, k, gs, zc=0, out_f32=True)
+    assert np.array_equal(got32.view(np.uint32), got16.view(np.uint32))
+    ref = orc.w4a16(a, qw, s, zw, 0, m, n, k, gs)
+    check_close(got32, ref, w4_tol(a, qw, s, zw, 0, n, k, gs), f"prefill f32 scales {m}x{n}")
+
+
 @pytest.mark.parametrize("per_group_zeros", [True, False])
 def test_w4a16_prefill_exact_integers(rt, dev, per_group_zeros):
     """Integer activations in [-3, 3] and power-of-two scales: every group's
