@@ -157,7 +157,7 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63;
-    const uint32_t wave = tid >> 6;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: DMA targets in SGPRs
     const uint32_t wm = wave / WN, wn = wave % WN;
 
     // ---- tile assignment -------------------------------------------------

@@ -433,6 +433,7 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
     using G = W4Cfg<BM, BN, WM, WN, STAGES>;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[G::SMEM];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t wave_s = __builtin_amdgcn_readfirstlane(wave);    // the same, in an SGPR (DMA targets, branches)
     const uint32_t wm = wave / WN, wn = wave % WN;
     const uint32_t M = p.M, N = p.N, K = p.K;
     const uint32_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
@@ -477,19 +478,19 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
         __amdgpu_buffer_rsrc_t rw = make_rsrc(W0 + (size_t)t * 64);
 #pragma unroll
         for (int j = 0; j < G::A_LOADS; j++)
-            dma_x4(ra, __builtin_amdgcn_readfirstlane(st + (wave * G::A_LOADS + j) * 1024), a_off[j]);
+            dma_x4(ra, __builtin_amdgcn_readfirstlane(st + (wave_s * G::A_LOADS + j) * 1024), a_off[j]);
 #pragma unroll
         for (int j = 0; j < G::W_LOADS; j++)
-            dma_x4(rw, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + (wave * G::W_LOADS + j) * 1024), w_off[j]);
-        if (wave == 0) {
+            dma_x4(rw, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + (wave_s * G::W_LOADS + j) * 1024), w_off[j]);
+        if (wave_s == 0) {
             __amdgpu_buffer_rsrc_t rs = make_rsrc(S0 + (size_t)t * N * 4);
             dma_x4(rs, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + G::W_BYTES), s_off);
-        } else if (wave == 1) {
+        } else if (wave_s == 1) {
             if (p.zeros) {
                 __amdgpu_buffer_rsrc_t rz = make_rsrc(p.zeros + (size_t)t * (N / 8) + n0 / 8);
                 dma_x1(rz, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + G::W_BYTES + G::Z_OFF), z_off);
             }
-        } else if (wave == G::NW - 1) {
+        } else if (wave_s == G::NW - 1) {
             __amdgpu_buffer_rsrc_t rx = make_rsrc(X + (size_t)t * M + m0);
             dma_x4(rx, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + G::W_BYTES + G::S_BYTES), x_off);
             if constexpr (BM * 4 > 1024)
