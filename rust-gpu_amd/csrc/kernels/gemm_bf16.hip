@@ -223,18 +223,32 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
         const bool tail = kt + BK > k_len;
         __amdgpu_buffer_rsrc_t ra = make_rsrc(A0 + (size_t)kt * 2);
         __amdgpu_buffer_rsrc_t rb = make_rsrc(NN ? B0 + (size_t)kt * ldb * 2 : B0 + (size_t)kt * 2);
+        // a full stage takes the precomputed offsets as they are; only the
+        // K tail masks per chunk (a uniform branch, so no selects otherwise)
+        if (!tail) {
+#pragma unroll
+            for (int j = 0; j < G::A_LOADS; j++)
+                if (j % nparts == part)
+                    dma_x4(ra, __builtin_amdgcn_readfirstlane(st + (wave * G::A_LOADS + j) * 1024), ld.a_off[j]);
+#pragma unroll
+            for (int j = 0; j < G::B_LOADS; j++)
+                if ((G::A_LOADS + j) % nparts == part)
+                    dma_x4(rb, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + (wave * G::B_LOADS + j) * 1024),
+                           ld.b_off[j]);
+            return;
+        }
 #pragma unroll
         for (int j = 0; j < G::A_LOADS; j++) {
             if (j % nparts != part) continue;
             uint32_t off = ld.a_off[j];
-            if (tail && kt + ld.a_kchunk[j] >= k_len) off = OOB_OFFSET;
+            if (kt + ld.a_kchunk[j] >= k_len) off = OOB_OFFSET;
             dma_x4(ra, __builtin_amdgcn_readfirstlane(st + (wave * G::A_LOADS + j) * 1024), off);
         }
 #pragma unroll
         for (int j = 0; j < G::B_LOADS; j++) {
             if ((G::A_LOADS + j) % nparts != part) continue;
             uint32_t off = ld.b_off[j];
-            if (tail && kt + ld.b_krow[j] >= k_len) off = OOB_OFFSET;
+            if (kt + ld.b_krow[j] >= k_len) off = OOB_OFFSET;
             dma_x4(rb, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + (wave * G::B_LOADS + j) * 1024), off);
         }
     };
