@@ -349,14 +349,18 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
     if (nk) load_frags(stage_ptr(0), 0, af[0], bfr[0]);
 
     if constexpr (KK % 2 == 0) {
-        for (uint32_t t = 0; t < nk; t++) {
+        // Steps with a successor take the barrier path unconditionally and
+        // the last step is peeled: with both paths in one loop body, the
+        // compiler's LDS wait at their join made every step's last MFMAs
+        // wait for the next step's fragment reads.
+        for (uint32_t t = 0; t + 1 < nk; t++) {
             const LDS_AS uint8_t* sa = stage_ptr(t);
 #pragma unroll
             for (int kk = 0; kk < KK; kk++) {
                 const int cur = kk & 1;
                 if (kk + 1 < KK) {
                     load_frags(sa, kk + 1, af[cur ^ 1], bfr[cur ^ 1]);
-                } else if (t + 1 < nk) {
+                } else {
                     // stage t+1 has landed once only the stages issued after
                     // it (t+2 .. t+STAGES-1) may still be in flight
                     if (t + STAGES - 1 < nk) wait_vmcnt<G::LOADS * (STAGES - 2)>();
@@ -365,6 +369,16 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
                     if (t + STAGES < nk) issue_stage(t + STAGES, 0, 1);
                     load_frags(stage_ptr(t + 1), 0, af[cur ^ 1], bfr[cur ^ 1]);
                 }
+                mfmas(af[cur], bfr[cur]);
+                order_substep();
+            }
+        }
+        if (nk) {
+            const LDS_AS uint8_t* sa = stage_ptr(nk - 1);
+#pragma unroll
+            for (int kk = 0; kk < KK; kk++) {
+                const int cur = kk & 1;
+                if (kk + 1 < KK) load_frags(sa, kk + 1, af[cur ^ 1], bfr[cur ^ 1]);
                 mfmas(af[cur], bfr[cur]);
                 order_substep();
             }
