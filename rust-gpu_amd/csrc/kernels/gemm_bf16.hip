@@ -344,6 +344,12 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
         if ((uint32_t)s < nk) issue_stage(s, 0, 1);
     if (nk >= STAGES) wait_vmcnt<G::LOADS * (STAGES - 1)>();
     else wait_vmcnt<0>();
+    // The epilogue's plane stride is loaded here, under the prologue
+    // barrier's wait: a scalar load still in flight at the K loop's entry
+    // (the compiler hoists it there) turns the first LDS wait of every step
+    // into a full one, since scalar loads complete out of order.
+    uint64_t y_split_stride = p.y_split_stride;
+    asm volatile("" : "+s"(y_split_stride));
     __syncthreads();
     bf16x8_t af[2][G::FM], bfr[2][G::FN];
     if (nk) load_frags(stage_ptr(0), 0, af[0], bfr[0]);
@@ -417,7 +423,7 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
     const uint32_t row_base = m0 + wm * G::TM, col_base = n0 + wn * G::TN;
 
     if (!fixup) {
-        Cb += (size_t)part * p.y_split_stride;
+        Cb += (size_t)part * y_split_stride;
 #pragma unroll
         for (int i = 0; i < G::FM; i++) {
 #pragma unroll
