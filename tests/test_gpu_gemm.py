@@ -163,6 +163,29 @@ def test_64x64_four_wave_tile(rt, dev, m, n, k, split):
             check_close(got, ref, tol, f"64x64 w4 {m}x{n}x{k} split {split} layout={layout} out={od}")
 
 
+@pytest.mark.parametrize("m,n,k", [(256, 256, 64), (300, 260, 128), (100, 700, 40), (256, 512, 200),
+                                   (513, 300, 1000), (256, 256, 4160)])
+def test_eight_wave_256_tiles(rt, dev, m, n, k):
+    """The 8-wave 256x256 instances (BK 64 with two stages: the 4096^3
+    kernel; BK 32 with four), reached by explicit configs (512 threads):
+    one, two and many K steps, K tails, ragged M / N, NN and NT, f32 and
+    bf16 out. Small-integer operands keep every partial sum exact, so the
+    f32 output must match the integer product bit for bit."""
+    rng = np.random.default_rng(m * 3 + n + k)
+    ai = rng.integers(-8, 9, size=(m, k))
+    bi = rng.integers(-6, 7, size=(k, n))
+    want = ai.astype(np.int64) @ bi.astype(np.int64)
+    a, b = bf16(ai), bf16(bi)
+    for base in (t0.GemmConfig.tile_256x256_k64(), t0.GemmConfig.tile_256x256_k32()):
+        cfg = base.copy(wg_size=512)
+        for layout, bb in ((t0.NN, b), (t0.NT, bf16(bi.T.copy()))):
+            got = run_gemm(rt, dev, a, bb, m, n, k, layout, t0.OUT_F32, cfg=cfg.copy(transpose=layout))
+            assert np.array_equal(got.astype(np.int64), want), (cfg.name(), m, n, k, layout)
+            got16 = run_gemm(rt, dev, a, bb, m, n, k, layout, t0.OUT_BF16,
+                             cfg=cfg.copy(transpose=layout, out_dtype=t0.OUT_BF16))
+            assert np.array_equal(got16, f32(orc.bf16_rne(want.astype(np.float32)))), (cfg.name(), m, n, k, layout)
+
+
 # ----------------------------------------------------------------- bounds --
 
 @pytest.mark.parametrize("m,n,k", [(33, 31, 40), (1, 1, 8), (255, 257, 264), (100, 200, 72), (300, 130, 1000)])
