@@ -215,6 +215,14 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
     }
 
     const uint32_t lds_base = (uint32_t)(uintptr_t)(LDS_AS uint8_t*)smem;
+    // With two waves per SIMD (8 waves, two stages), only waves 0..NW/2-1
+    // issue the DMAs of a full stage of an interior tile: theirs and those of
+    // wave + NW/2, whose chunks sit BM/2 rows of A and BK/2 k-rows (NN) or
+    // BN/2 rows (NT) of B further on, at the same per-lane offsets.  An LDS-DMA
+    // instruction holds its wave for tens of cycles at issue; this way the
+    // other wave on each SIMD keeps the MFMA pipe busy meanwhile.
+    constexpr bool PAIR_DMA = G::NW == 8 && STAGES == 2;
+    const bool pair_dma = PAIR_DMA && m0 + BM <= M && n0 + BN <= N;
     // Issues the loads q of stage t with q % nparts == part (A loads first,
     // then B), so a stage can go out in slices between MFMA groups.
     auto issue_stage = [&](uint32_t t, int part, int nparts) {
@@ -223,6 +231,27 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
         const bool tail = kt + BK > k_len;
         __amdgpu_buffer_rsrc_t ra = make_rsrc(A0 + (size_t)kt * 2);
         __amdgpu_buffer_rsrc_t rb = make_rsrc(NN ? B0 + (size_t)kt * ldb * 2 : B0 + (size_t)kt * 2);
+        if (PAIR_DMA && pair_dma && !tail && nparts == 1) {
+            if (wave < G::NW / 2) {
+                constexpr uint32_t HA = G::NW / 2 * G::A_LOADS * 1024, HB = G::NW / 2 * G::B_LOADS * 1024;
+                __amdgpu_buffer_rsrc_t ra2 = make_rsrc(A0 + (size_t)kt * 2 + (size_t)(BM / 2) * lda * 2);
+                __amdgpu_buffer_rsrc_t rb2 = make_rsrc(NN ? B0 + (size_t)(kt + BK / 2) * ldb * 2
+                                                          : B0 + (size_t)kt * 2 + (size_t)(BN / 2) * ldb * 2);
+#pragma unroll
+                for (int j = 0; j < G::A_LOADS; j++) {
+                    dma_x4(ra, __builtin_amdgcn_readfirstlane(st + (wave * G::A_LOADS + j) * 1024), ld.a_off[j]);
+                    dma_x4(ra2, __builtin_amdgcn_readfirstlane(st + HA + (wave * G::A_LOADS + j) * 1024), ld.a_off[j]);
+                }
+#pragma unroll
+                for (int j = 0; j < G::B_LOADS; j++) {
+                    dma_x4(rb, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + (wave * G::B_LOADS + j) * 1024),
+                           ld.b_off[j]);
+                    dma_x4(rb2, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + HB + (wave * G::B_LOADS + j) * 1024),
+                           ld.b_off[j]);
+                }
+            }
+            return;
+        }
         // a full stage takes the precomputed offsets as they are; only the
         // K tail masks per chunk (a uniform branch, so no selects otherwise)
         if (!tail) {
