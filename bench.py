@@ -65,22 +65,48 @@ class Timer:
         self.rt.wait_idle()
         return self.e0.elapsed_ms(self.e1) / steps
 
+    def per_call(self, fn, n: int) -> list:
+        """ms of each of n calls, an event pair around every call (the GPU is
+        already warm from run()); the event records themselves add a little."""
+        evs = [t0.Event() for _ in range(n + 1)]
+        evs[0].record(self.rt)
+        for i in range(n):
+            fn()
+            evs[i + 1].record(self.rt)
+        evs[-1].synchronize()
+        return [evs[i].elapsed_ms(evs[i + 1]) for i in range(n)]
+
 
 USE_GRAPHS = True
 
 
-def rotate_timed(rt, one, steps, warmup) -> float:
-    """ms per launch of one(i) over ROTATE buffer sets: the ROTATE launches are
-    captured in a HIP graph and replayed (launch overhead stays off the GPU
-    timeline), or issued directly with --no-graph (for tracing tools)."""
+def rotate_timed(rt, one, steps, warmup):
+    """(mean, median) ms per launch of one(i) over ROTATE buffer sets: the
+    ROTATE launches are captured in a HIP graph and replayed (launch overhead
+    stays off the GPU timeline), or issued directly with --no-graph (for
+    tracing tools).  The median is over per-replay times."""
     if USE_GRAPHS:
         g = rt.capture(lambda: [one(i) for i in range(ROTATE)])
-        return Timer(rt).run(g.launch, steps, warmup) / ROTATE
+        fn = g.launch
+    else:
+        def fn():
+            for i in range(ROTATE):
+                one(i)
+    tm = Timer(rt)
+    mean = tm.run(fn, steps, warmup) / ROTATE
+    med = float(np.median(tm.per_call(fn, max(10, steps)))) / ROTATE
+    return mean, med
 
-    def all_sets():
-        for i in range(ROTATE):
-            one(i)
-    return Timer(rt).run(all_sets, steps, warmup) / ROTATE
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 def bench_copy(rt, steps, warmup, rng, tr):
@@ -126,13 +152,25 @@ def bench_gemm_4096(rt, steps, warmup, rng, tr):
         rt.gemm(da.gpu_addr(), db.gpu_addr(), dc.gpu_addr(), m, n, k, transpose=t0.NN, out_dtype=t0.OUT_BF16,
                 cfg=cfg)
 
-    ms = Timer(rt).run(step, steps, warmup)
+    tm = Timer(rt)
+    ms = tm.run(step, steps, warmup)
+    per = tm.per_call(step, max(100, steps))
+    # measured shader clock under this load: per-workgroup s_memtime against
+    # the 100 MHz real-time clock, median over workgroups, over 5 launches
+    probes = [rt.gemm_clock_probe(da.gpu_addr(), db.gpu_addr(), dc.gpu_addr(), m, n, k, transpose=t0.NN,
+                                  out_dtype=t0.OUT_BF16, cfg=cfg) for _ in range(5)]
+    sclk = float(np.median([p[0] for p in probes]))
+    span = float(np.median([p[1] for p in probes]))
     flops = 2.0 * m * n * k
     tflops = flops / (ms * 1e-3) / 1e12
     for buf in (da, db, dc):
         buf.free()
-    return {"ms": ms, "tflops": tflops, "kernel": cfg.name(), "a": a, "b": b,
-            "roofline": roofline("mfma", tflops, PEAK_TFLOPS, "TFLOP/s", traffic_of(tr, "gemm_4096_nn_bf16"))}
+    rf = roofline("mfma", tflops, PEAK_TFLOPS, "TFLOP/s", traffic_of(tr, "gemm_4096_nn_bf16"))
+    rf["sclk_mhz_measured"] = round(sclk, 1)
+    rf["peak_at_measured_sclk"] = round(PEAK_TFLOPS * sclk / 2400.0, 1)
+    rf["frac_at_measured_sclk"] = round(tflops / (PEAK_TFLOPS * sclk / 2400.0), 4)
+    return {"ms": ms, "ms_median_per_launch": float(np.median(per)), "tflops": tflops, "kernel": cfg.name(),
+            "a": a, "b": b, "sclk_mhz": sclk, "workgroup_span_us": span, "roofline": rf}
 
 
 def bench_skinny(rt, steps, warmup, rng, tr):
@@ -149,14 +187,16 @@ def bench_skinny(rt, steps, warmup, rng, tr):
 
     one(0)
     rt.wait_idle()
-    ms = rotate_timed(rt, one, steps, warmup)
+    b0 = bs[0].read(np.uint16, k * n).reshape(k, n)
+    ms, med = rotate_timed(rt, one, steps, warmup)
     bytes_alg = m * k * 2 + k * n * 2 + m * n * 2
     gbs = bytes_alg / (ms * 1e-3) / 1e9
     tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
     for buf in bs + [da, dc]:
         buf.free()
     return {"workload": "skinny bf16 GEMM M=128 N=4096 K=4096 NN, bf16 out", "kernel": cfg.name(),
-            "us_per_launch": round(ms * 1e3, 3), "tflops": round(tflops, 2), "gbs": round(gbs, 1),
+            "us_per_launch": round(ms * 1e3, 3), "us_median_per_launch": round(med * 1e3, 3),
+            "tflops": round(tflops, 2), "gbs": round(gbs, 1), "_host": (a, b0),
             "roofline": roofline("hbm", gbs, PEAK_GBS, "GB/s", traffic_of(tr, "gemm_skinny_128x4096x4096"))}
 
 
@@ -178,10 +218,12 @@ def _w4_operands(rng, n, k, gs, per_group_zeros):
 
 def bench_decode(rt, steps, warmup, rng, tr):
     m, n, k, gs = 16, 11008, 4096, 128
-    a = rt.upload(bf16_rne(rng.standard_normal((m, k), dtype=np.float32)))
-    sets = []
+    a_h = bf16_rne(rng.standard_normal((m, k), dtype=np.float32))
+    a = rt.upload(a_h)
+    sets, host0 = [], None
     for _ in range(ROTATE):
         qw, s, _ = _w4_operands(rng, n, k, gs, False)
+        host0 = host0 or (qw, s)
         sets.append((rt.upload(qw), rt.upload(s)))
     dc = rt.alloc(m * n * 2)
 
@@ -193,7 +235,7 @@ def bench_decode(rt, steps, warmup, rng, tr):
                          group_size=gs, zero_const=8)
     one(0)
     rt.wait_idle()
-    ms = rotate_timed(rt, one, steps, warmup)
+    ms, med = rotate_timed(rt, one, steps, warmup)
     # algorithmic bytes: W nibbles + bf16 scales + A + C (constant z not stored)
     bytes_alg = n * k // 2 + (k // gs) * n * 2 + m * k * 2 + m * n * 2
     gbs = bytes_alg / (ms * 1e-3) / 1e9
@@ -203,14 +245,15 @@ def bench_decode(rt, steps, warmup, rng, tr):
     a.free()
     dc.free()
     return {"workload": "W4A16 decode M=16 K=4096 N=11008, g=128, z=8, bf16 out", "kernel": plan[0],
-            "split_k": plan[1], "us_per_launch": round(ms * 1e3, 3), "gbs": round(gbs, 1),
-            "bytes_per_launch": bytes_alg,
+            "split_k": plan[1], "us_per_launch": round(ms * 1e3, 3), "us_median_per_launch": round(med * 1e3, 3),
+            "gbs": round(gbs, 1), "bytes_per_launch": bytes_alg, "_host": (a_h, host0[0], host0[1]),
             "roofline": roofline("hbm", gbs, PEAK_GBS, "GB/s", traffic_of(tr, "w4a16_decode_16x4096x11008"))}
 
 
 def bench_prefill(rt, steps, warmup, rng, tr):
     m, n, k, gs = 4096, 14336, 4096, 128
-    a = rt.upload(bf16_rne(rng.standard_normal((m, k), dtype=np.float32)))
+    a_h = bf16_rne(rng.standard_normal((m, k), dtype=np.float32))
+    a = rt.upload(a_h)
     qw, s, zw = _w4_operands(rng, n, k, gs, True)
     dq, ds, dz = rt.upload(qw), rt.upload(s), rt.upload(zw)
     dc = rt.alloc(m * n * 2)
@@ -221,12 +264,15 @@ def bench_prefill(rt, steps, warmup, rng, tr):
 
     plan = rt.w4a16_plan(a.gpu_addr(), dq.gpu_addr(), ds.gpu_addr(), dz.gpu_addr(), dc.gpu_addr(), m, n, k,
                          group_size=gs, zero_const=0)
-    ms = Timer(rt).run(step, max(5, steps // 4), max(2, warmup // 2))
+    tm = Timer(rt)
+    ms = tm.run(step, max(5, steps // 4), max(2, warmup // 2))
+    med = float(np.median(tm.per_call(step, 20)))
     tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
     for buf in (a, dq, ds, dz, dc):
         buf.free()
     return {"workload": "W4A16 prefill M=4096 K=4096 N=14336, g=128, per-group z, bf16 out", "kernel": plan[0],
-            "ms_per_launch": round(ms, 4), "tflops": round(tflops, 2),
+            "ms_per_launch": round(ms, 4), "ms_median_per_launch": round(med, 4), "tflops": round(tflops, 2),
+            "_host": (a_h, qw, s, zw),
             "roofline": roofline("mfma", tflops, PEAK_TFLOPS, "TFLOP/s", traffic_of(tr, "w4a16_prefill_4096x4096x14336"))}
 
 
@@ -294,8 +340,8 @@ def bench_norm_decode(rt, steps, warmup, rng, tr):
     fused(0)
     separate(0)
     rt.wait_idle()
-    ms_f = rotate_timed(rt, fused, steps, warmup)
-    ms_s = rotate_timed(rt, separate, steps, warmup)
+    ms_f, _ = rotate_timed(rt, fused, steps, warmup)
+    ms_s, _ = rotate_timed(rt, separate, steps, warmup)
     for buf in [res, hid, gam, x2, a16, dc] + [b for st in sets for b in st]:
         buf.free()
     return {"workload": "decode token: residual + RMSNorm + W4A16 M=1 K=4096 N=11008, g=128, z=8",
@@ -303,21 +349,83 @@ def bench_norm_decode(rt, steps, warmup, rng, tr):
             "us_two_kernels": round(ms_s * 1e3, 3)}
 
 
-def cpu_baseline(a, b, rows: int):
-    """The reference CPU matmul (oracle restatement, one thread) on rows
-    [0, rows) of the 4096^3 product, scaled to the whole product."""
+def _cpu_entry(value, unit, sample, secs, extra=None):
+    d = {"value": value, "unit": unit, "cores": 1, "kind": "port", "sample": sample, "seconds": round(secs, 2),
+         "host": cpu_model(), "nproc": os.cpu_count()}
+    if extra:
+        d.update(extra)
+    return d
+
+
+LOOP = "sequential-f32 no-FMA loop of examples/test_gemm_correctness.rs:28-42 (oracle restatement, one thread)"
+
+
+def cpu_baselines(head, extras, rows_big: int):
+    """The reference's CPU path on every BASELINE config (the same seeded
+    inputs as the GPU run, in this process): C1 256^3 and C3 skinny in full;
+    C4 decode in full as dequant (src/t0/quant_kernels.rs:365-372) then the
+    same loop; C2 4096^3 and C5 prefill on a contiguous slice of rows_big M
+    rows, scaled by M / rows_big (the naive loop's cost is linear in M)."""
     from oracle import oracle as orc   # checker-side code: the CPU baseline leg only
+    out = {}
+    # C2: 4096^3 NN, bf16 inputs N(0,1)
+    a, b = head["a"], head["b"]
     m, k = a.shape
     n = b.shape[1]
     t = time.perf_counter()
-    orc.gemm_rows(a, b, "nn", 0, rows)
+    orc.gemm_rows(a, b, "nn", 0, rows_big)
     dt = time.perf_counter() - t
-    tflops = 2.0 * rows * n * k / dt / 1e12
-    return {"value": tflops, "unit": "TFLOP/s", "cores": 1, "kind": "port",
-            "sample": f"rows 0-{rows - 1} of the 4096^3 NN GEMM ({2.0 * rows * n * k / 1e9:.2f} GFLOP, "
-                      f"{dt:.1f} s), sequential-f32 no-FMA loop of examples/test_gemm_correctness.rs:28-42; "
-                      f"the naive loop's cost is linear in rows, so the rate holds for all {m} rows",
-            "host": platform.processor() or platform.machine(), "nproc": os.cpu_count()}
+    out["gemm_4096"] = _cpu_entry(2.0 * rows_big * n * k / dt / 1e12, "TFLOP/s",
+                                  f"rows 0-{rows_big - 1} of the 4096^3 NN GEMM ({2.0 * rows_big * n * k / 1e9:.2f} "
+                                  f"GFLOP), {LOOP}; scaled to all {m} rows (cost linear in rows): "
+                                  f"{dt * m / rows_big:.0f} s for the whole GEMM", dt)
+    # C1: 256^3, U(-1,1) inputs, f32 out, in full
+    rng = np.random.default_rng(256)
+    a1 = bf16_rne(rng.uniform(-1, 1, (256, 256)).astype(np.float32))
+    b1 = bf16_rne(rng.uniform(-1, 1, (256, 256)).astype(np.float32))
+    t = time.perf_counter()
+    orc.gemm_nn(a1, b1)
+    dt = time.perf_counter() - t
+    out["gemm_256"] = _cpu_entry(2.0 * 256 ** 3 / dt / 1e12, "TFLOP/s", f"whole 256^3 GEMM (U(-1,1) seed 256), {LOOP}",
+                                 dt)
+    # C3: skinny 128x4096x4096, in full
+    if "skinny" in extras:
+        a3, b3 = extras["skinny"]["_host"]
+        t = time.perf_counter()
+        orc.gemm_nn(a3, b3)
+        dt = time.perf_counter() - t
+        fl = 2.0 * 128 * 4096 * 4096
+        by = 128 * 4096 * 2 + 4096 * 4096 * 2 + 128 * 4096 * 2
+        out["skinny"] = _cpu_entry(fl / dt / 1e12, "TFLOP/s", f"whole 128x4096x4096 GEMM (weight set 0), {LOOP}", dt,
+                                   {"gbs": round(by / dt / 1e9, 4)})
+    # C4: decode, dequant + loop, in full
+    if "w4a16_decode" in extras:
+        a4, qw, sc = extras["w4a16_decode"]["_host"]
+        mm, kk, nn_ = a4.shape[0], a4.shape[1], qw.shape[0]
+        t = time.perf_counter()
+        w = orc.w4a16_dequant(qw, sc, None, 8, nn_, kk, 128)
+        orc.gemm_bf16_f32w_rows(a4, w, 0, mm)
+        dt = time.perf_counter() - t
+        by = extras["w4a16_decode"]["bytes_per_launch"]
+        out["w4a16_decode"] = _cpu_entry(by / dt / 1e9, "GB/s",
+                                         f"whole 16x4096x11008 decode (weight set 0): dequant (q - 8) * s to f32, then "
+                                         f"{LOOP}; GB/s of the same algorithmic bytes ({by})", dt,
+                                         {"tflops": round(2.0 * mm * nn_ * kk / dt / 1e12, 6)})
+    # C5: prefill, dequant + a row slice of the loop
+    if "w4a16_prefill" in extras:
+        a5, qw, sc, zw = extras["w4a16_prefill"]["_host"]
+        mm, kk, nn_ = a5.shape[0], a5.shape[1], qw.shape[0]
+        t = time.perf_counter()
+        w = orc.w4a16_dequant(qw, sc, zw, 0, nn_, kk, 128)
+        t_dq = time.perf_counter() - t
+        orc.gemm_bf16_f32w_rows(a5, w, 0, rows_big)
+        t_loop = time.perf_counter() - t - t_dq
+        total = t_dq + t_loop * mm / rows_big
+        out["w4a16_prefill"] = _cpu_entry(2.0 * mm * nn_ * kk / total / 1e12, "TFLOP/s",
+                                          f"dequant of the whole 14336x4096 weight ({t_dq:.1f} s) + rows 0-{rows_big - 1}"
+                                          f" of {LOOP} ({t_loop:.1f} s), the loop scaled to all {mm} rows: "
+                                          f"{total:.0f} s for the whole prefill", t_dq + t_loop)
+    return out
 
 
 def main():
@@ -325,7 +433,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--cpu-rows", type=int, default=256)
+    ap.add_argument("--cpu-rows", type=int, default=64, help="M rows of the 4096^3 and prefill CPU samples")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="issue rotated launches directly (for tracers)")
@@ -350,8 +458,8 @@ def main():
               "prefill": bench_prefill, "ignis": bench_ignis, "norm_decode": bench_norm_decode,
               "copy": bench_copy}[args.only]
         r = fn(rt, args.steps, args.warmup, rng, tr)
-        r.pop("a", None)
-        r.pop("b", None)
+        for key in ("a", "b", "_host"):
+            r.pop(key, None)
         print(json.dumps({"only": args.only, **{k: v for k, v in r.items()}}, default=float), flush=True)
         rt.close()
         return
@@ -364,10 +472,18 @@ def main():
         for name, fn in (("skinny", bench_skinny), ("w4a16_decode", bench_decode), ("w4a16_prefill", bench_prefill),
                          ("ignis_matmul", bench_ignis), ("norm_decode", bench_norm_decode)):
             extras[name] = fn(rt, args.steps, args.warmup, rng, tr)
-            print(f"# {name}: {json.dumps(extras[name])}", file=sys.stderr, flush=True)
+            shown = {k: v for k, v in extras[name].items() if k != "_host"}
+            print(f"# {name}: {json.dumps(shown)}", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(head["a"], head["b"], args.cpu_rows)
+        cpus = cpu_baselines(head, extras, args.cpu_rows)
+        cpu = cpus.pop("gemm_4096")
+        extras["cpu_gemm_256"] = {"workload": "bf16 GEMM M=N=K=256, U(-1,1), f32 out (CPU-only config)",
+                                  "cpu_baseline": cpus.pop("gemm_256")}
+        for key, v in cpus.items():
+            extras[key]["cpu_baseline"] = v
+    for e in extras.values():
+        e.pop("_host", None)
     rt.close()
 
     line = {
@@ -378,6 +494,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(head["ms"], 5),
+        "ms_median_per_launch": round(head["ms_median_per_launch"], 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -385,7 +502,8 @@ def main():
         "data": "synthetic: N(0,1) rounded to bf16 (numpy seed 20261201), inputs resident in HBM",
         "config": {"workload": "bf16 GEMM M=N=K=4096, A[M,K] . B[K,N] row-major (NN), fp32 accumulate, bf16 out",
                    "m": 4096, "n": 4096, "k": 4096, "layout": "NN", "out": "bf16", "kernel": head["kernel"],
-                   "device": info},
+                   "device": info, "sclk_mhz_measured": round(head["sclk_mhz"], 1),
+                   "workgroup_span_us": round(head["workgroup_span_us"], 2)},
         "roofline": head["roofline"],
         "cpu_baseline": cpu,
         "extras": extras,

@@ -295,6 +295,15 @@ typedef struct t0_gemm_desc {
 int t0_gemm(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm_desc* d);
 /* The config t0_gemm would use for d (NULL cfg). */
 int t0_gemm_select(t0_runtime* rt, const t0_gemm_desc* d, t0_gemm_config* out);
+/* Measurement aid with no counterpart in the reference (its README quotes
+ * the nominal clock only): runs t0_gemm once with per-workgroup timestamps
+ * (shader clock and the 100 MHz real-time clock at each workgroup's start and
+ * end), waits, and returns the median shader clock over workgroups in MHz and
+ * the span from the first start to the last end in microseconds.  Tiled
+ * kernels without split-K only (else T0_ERR_INVALID); at most 65536
+ * workgroups.  Synchronous. */
+int t0_gemm_clock_probe(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm_desc* d, double* sclk_mhz,
+                        double* span_us);
 
 /* Replaces auto_gemm::GemmTuner::tune (src/t0/auto_gemm.rs:82-216) and the
  * JSON cache (src/t0/auto_gemm.rs:435-501): benchmark candidate configs on

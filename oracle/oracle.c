@@ -276,6 +276,26 @@ void orc_w4a16(const uint16_t* a, const uint32_t* qw, const uint16_t* scales,
     orc_w4a16_rows(a, qw, scales, zeros, zc, y, 0, m, n, k, gs);
 }
 
+/* The reference CPU loop on bf16 activations and already dequantized f32
+ * weights w [N][K]: y[i,j] = sum_k bf16(a[i,k]) * w[j,k], f32 in k order, no
+ * FMA.  With w from orc_w4a16_dequant this is "dequant, then the same loop"
+ * (src/t0/quant_kernels.rs:365-372 + examples/test_gemm_correctness.rs:28-42)
+ * and equals orc_w4a16_rows bit for bit (same products, same order). */
+void orc_gemm_bf16_f32w_rows(const uint16_t* a, const float* w, float* y,
+                             size_t row0, size_t row1, size_t n, size_t k)
+{
+    for (size_t i = row0; i < row1; i++)
+        for (size_t j = 0; j < n; j++) {
+            float acc = 0.0f;
+            const float* wr = w + j * k;
+            for (size_t kk = 0; kk < k; kk++) {
+                float p = orc_bf16_to_f32(a[i * k + kk]) * wr[kk];
+                acc = acc + p;
+            }
+            y[i * n + j] = acc;
+        }
+}
+
 /* Dequantize the W4A16 operand to an f32 [N][K] matrix (exact). */
 void orc_w4a16_dequant(const uint32_t* qw, const uint16_t* scales,
                        const uint32_t* zeros, uint32_t zc, float* w,

@@ -69,6 +69,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_w4a16_rows.argtypes = [_P, _P, _P, _P, ctypes.c_uint32, _P, _SZ, _SZ, _SZ, _SZ, _SZ]
     L.orc_w4a16.argtypes = [_P, _P, _P, _P, ctypes.c_uint32, _P, _SZ, _SZ, _SZ, _SZ]
     L.orc_w4a16_dequant.argtypes = [_P, _P, _P, ctypes.c_uint32, _P, _SZ, _SZ, _SZ]
+    L.orc_gemm_bf16_f32w_rows.argtypes = [_P, _P, _P, _SZ, _SZ, _SZ, _SZ]
     L.orc_rmsnorm_rows.argtypes = [_P, _P, _P, _P, _P, _P, _SZ, _SZ, ctypes.c_float]
     L.orc_ffn_fused_rmsnorm_gemm.argtypes = [_P, _P, _P, _P, _P, _SZ, _SZ, ctypes.c_float]
 
@@ -257,6 +258,18 @@ def w4a16(a, qw, scales, zeros, zc, m, n, k, gs, row0=0, row1=None) -> np.ndarra
     y = np.zeros((row1 - row0, n), dtype=np.float32)
     base = y.ctypes.data - row0 * n * 4
     lib().orc_w4a16_rows(_ptr(a), _ptr(qw), _ptr(scales), _ptr(zeros), zc, base, row0, row1, n, k, gs)
+    return y
+
+
+def gemm_bf16_f32w_rows(a: np.ndarray, w: np.ndarray, row0: int, row1: int) -> np.ndarray:
+    """Rows [row0, row1) of the reference loop on bf16 a [M][K] and f32 w [N][K]
+    (dequantized weights).  Ref: examples/test_gemm_correctness.rs:28-42."""
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    n, k = w.shape
+    y = np.zeros((row1 - row0, n), dtype=np.float32)
+    base = y.ctypes.data - row0 * n * 4
+    lib().orc_gemm_bf16_f32w_rows(_ptr(a), _ptr(w), base, row0, row1, n, k)
     return y
 
 

@@ -68,6 +68,7 @@ struct t0_runtime {
     size_t stage_bytes = 0;
     uint32_t* sem = nullptr;
     size_t sem_count = 0;
+    void* probe = nullptr;          // t0_gemm_clock_probe timestamps
     // Held for the host side of every call that uses ws / stage / sem, so
     // that threads sharing the runtime never resize a buffer another call
     // has just put into its kernel arguments (recursive: calls nest).
@@ -299,6 +300,7 @@ int t0_runtime_destroy(t0_runtime* rt) {
     if (rt->ws) hipFree(rt->ws);
     if (rt->stage) hipFree(rt->stage);
     if (rt->sem) hipFree(rt->sem);
+    if (rt->probe) hipFree(rt->probe);
     if (rt->module) hipModuleUnload(rt->module);
     if (rt->own_stream) hipStreamDestroy(rt->own_stream);
     delete rt;
@@ -758,7 +760,8 @@ int t0_gemm_select(t0_runtime* rt, const t0_gemm_desc* d, t0_gemm_config* out) {
     return T0_OK;
 }
 
-int t0_gemm(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm_desc* d) {
+static int gemm_impl(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm_desc* d, uint64_t* clock_probe,
+                     uint32_t* workgroups) {
     if (!rt || !d) return fail(T0_ERR_INVALID, "null argument");
     std::lock_guard<std::recursive_mutex> call_lock(rt->call_mu);
     if (!d->m || !d->n || !d->k) return fail(T0_ERR_INVALID, "empty GEMM %ux%ux%u", d->m, d->n, d->k);
@@ -779,7 +782,51 @@ int t0_gemm(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm_desc* d) {
     r = set_dev(rt);
     if (r) return r;
     if (p.split_k > 1 && !fast_ok(p, d->transpose == T0_NN)) p.split_k = 1, p.flags &= ~T0_GEMM_FIXUP;
+    if (clock_probe) {
+        if (p.split_k > 1 || !fast_ok(p, d->transpose == T0_NN))
+            return fail(T0_ERR_INVALID, "the clock probe needs a tiled kernel without split-K");
+        const uint32_t wgs = ((p.M + g->bm - 1) / g->bm) * ((p.N + g->bn - 1) / g->bn);
+        if (wgs > *workgroups) return fail(T0_ERR_INVALID, "clock probe: %u workgroups, at most %u", wgs, *workgroups);
+        p.clock_probe = clock_probe;
+        *workgroups = wgs;
+    }
     return run_gemm_params(rt, g, d->transpose == T0_NN, p);
+}
+
+int t0_gemm(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm_desc* d) {
+    return gemm_impl(rt, cfg, d, nullptr, nullptr);
+}
+
+int t0_gemm_clock_probe(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm_desc* d, double* sclk_mhz,
+                        double* span_us) {
+    if (!rt || !d || !sclk_mhz || !span_us) return fail(T0_ERR_INVALID, "null argument");
+    std::lock_guard<std::recursive_mutex> call_lock(rt->call_mu);
+    const size_t max_wg = 65536;
+    if (!rt->probe) {
+        int r = set_dev(rt);
+        if (r) return r;
+        HIPCHK(hipMalloc(&rt->probe, max_wg * 32));
+    }
+    uint32_t wgs = (uint32_t)max_wg;   // in: capacity of the timestamp buffer, out: workgroups launched
+    int r = gemm_impl(rt, cfg, d, (uint64_t*)rt->probe, &wgs);
+    if (r) return r;
+    std::vector<uint64_t> ts((size_t)wgs * 4);
+    HIPCHK(hipStreamSynchronize(rt->stream));
+    HIPCHK(hipMemcpy(ts.data(), rt->probe, ts.size() * 8, hipMemcpyDeviceToHost));
+    std::vector<double> mhz;
+    uint64_t first = ~0ull, last = 0;
+    for (uint32_t w = 0; w < wgs; w++) {
+        const uint64_t rt0 = ts[4 * w], rt1 = ts[4 * w + 1], c0 = ts[4 * w + 2], c1 = ts[4 * w + 3];
+        if (rt1 <= rt0) continue;
+        mhz.push_back((double)(c1 - c0) / (double)(rt1 - rt0) * 100.0);   // s_memrealtime counts at 100 MHz
+        first = std::min(first, rt0);
+        last = std::max(last, rt1);
+    }
+    if (mhz.empty()) return fail(T0_ERR_HIP, "clock probe: no workgroup recorded its timestamps");
+    std::sort(mhz.begin(), mhz.end());
+    *sclk_mhz = mhz[mhz.size() / 2];
+    *span_us = (double)(last - first) / 100.0;
+    return T0_OK;
 }
 
 // ------------------------------------------------------------------ tuner --

@@ -36,6 +36,8 @@ typedef struct t0_gemm_params {
     const float* bias;    // [N] f32 (T0_EPI_BIAS)
     float* workspace;     // fixup planes [split_k][tiles][BM*BN] f32
     uint32_t* semaphores; // fixup counters [tiles]
+    uint64_t* clock_probe;    // NULL, or [workgroups][4]: 100 MHz clock at start / end,
+                              // shader clock at start / end (workgroup's thread 0)
     uint32_t M, N, K;
     uint32_t lda, ldb, ldc;
     uint32_t split_k;          // >= 1

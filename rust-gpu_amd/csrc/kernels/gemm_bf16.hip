@@ -168,6 +168,11 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
     const uint32_t total = tiles * sk;
     const uint32_t bid = blockIdx.y * gridDim.x + blockIdx.x;
     if (bid >= total) return;
+    uint64_t* const probe = p.clock_probe;
+    if (probe && tid == 0) {
+        probe[4 * bid] = __builtin_amdgcn_s_memrealtime();
+        probe[4 * bid + 2] = __builtin_amdgcn_s_memtime();
+    }
     const uint32_t lid = xcd_remap(bid, total);
     const uint32_t part = lid / tiles;
     const uint32_t tile_id = lid % tiles;
@@ -463,6 +468,10 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
                     *(LDS_AS f32x4_t*)(wreg + l32 * G::EPI_LD + j * 32 + 8 * g + 4 * hi) = v;
                 }
             emit_rowblock<G>(p, Cb, wreg, row_base + i * 32, col_base, lane);
+        }
+        if (probe && tid == 0) {
+            probe[4 * bid + 1] = __builtin_amdgcn_s_memrealtime();
+            probe[4 * bid + 3] = __builtin_amdgcn_s_memtime();
         }
         return;
     }

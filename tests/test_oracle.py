@@ -412,6 +412,20 @@ def test_w4a16_per_group_zeros_and_scales():
     assert np.all(np.abs(y - exact) <= bound + 1e-30)
     # rows slice
     assert np.array_equal(orc.w4a16(a, qw, s, zw, 0, m, n, k, gs, 1, 3), y[1:3])
+    # "dequant, then the same loop" (the CPU-baseline path) gives the same bits
+    assert np.array_equal(orc.gemm_bf16_f32w_rows(a, w, 0, m).view(np.uint32), y.view(np.uint32))
+    assert np.array_equal(orc.gemm_bf16_f32w_rows(a, w, 1, 3).view(np.uint32), y[1:3].view(np.uint32))
+
+
+def test_gemm_bf16_f32w_sequential_order():
+    """The dequantized-weight loop sums in k order without FMA: on
+    a = [1, 1, 1], w = [1, 2^27, -2^27] the f32 sum is (1 + 2^27) - 2^27 = 0
+    (the 1 is absorbed), while a reordered or wider sum would give 1."""
+    a = orc.bf16_rne(np.ones((1, 3), np.float32))
+    w = np.array([[1.0, 2.0**27, -(2.0**27)]], np.float32)
+    assert orc.gemm_bf16_f32w_rows(a, w, 0, 1)[0, 0] == 0.0
+    w2 = np.array([[2.0**27, -(2.0**27), 1.0]], np.float32)
+    assert orc.gemm_bf16_f32w_rows(a, w2, 0, 1)[0, 0] == 1.0
 
 
 # ----------------------------------------------------------- GPTQ bytes --
