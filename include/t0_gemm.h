@@ -269,7 +269,12 @@ int t0_event_elapsed_ms(const t0_event* start, const t0_event* stop, float* ms);
  * DispatchQueue batches AQL packets, src/t0/prefill_dispatch.rs:61-130):
  * everything launched on the runtime's stream between begin and end is
  * recorded, then replayed with one launch.  Workspaces must already exist
- * (run the same calls once before capturing). */
+ * (run the same calls once before capturing): a call that would grow the
+ * runtime's split-K workspace, semaphore array or operand staging buffer
+ * fails with T0_ERR_INVALID during capture, and also while any graph made
+ * from this runtime exists, since the graph's kernels hold those addresses
+ * (a graph pins the workspace size until t0_graph_destroy).  Destroy graphs
+ * before their runtime; one that outlives it can still be destroyed. */
 typedef struct t0_graph t0_graph;
 int t0_graph_begin(t0_runtime* rt);
 int t0_graph_end(t0_runtime* rt, t0_graph** out);
@@ -307,13 +312,30 @@ int t0_gemm_clock_probe(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm
 
 /* Replaces auto_gemm::GemmTuner::tune (src/t0/auto_gemm.rs:82-216) and the
  * JSON cache (src/t0/auto_gemm.rs:435-501): benchmark candidate configs on
- * the device (hipEvent timing, median) after a 256^3 correctness smoke test,
- * cache the winner in memory and at <cache_dir>/gemm_<arch>_<MxNxK>_<layout>_<out>.json.
+ * the device (hipEvent timing on seeded N(0,1) bf16 operands, median) after a
+ * 256^3 correctness smoke test, cache the winner in memory and on disk in the
+ * reference's JSON layout (tile_m, tile_n, tile_k, wg_size, split_k, lds_pad,
+ * n_col_passes, wgp, swap, tflops, all; plus arch, transpose, out_dtype,
+ * name).  NT with f32 output keeps the reference's file name
+ * <cache_dir>/gemm_<M>x<N>x<K>.json (reference cache files load); other
+ * layouts add _<nn|nt>_<bf16|f32>.  A file is used only if a gfx950 kernel
+ * runs its config (tile and wave count, split_k a power of two <= 16) and it
+ * names no other architecture; otherwise the candidates are ranked afresh.
  * cfg_out/tflops_out may be NULL. */
 int t0_tune(t0_runtime* rt, uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype,
             t0_gemm_config* cfg_out, double* tflops_out);
 int t0_tuner_set_cache_dir(const char* dir);
 int t0_tuner_set_params(uint32_t max_candidates, uint32_t n_iters);
+/* The on-disk cache without a runtime (gfx950 entries), after
+ * GemmTuner::save_cache / load_cache / invalidate (src/t0/auto_gemm.rs:439-507):
+ * store writes cfg (T0_ERR_INFEASIBLE if no gfx950 kernel runs it); load
+ * returns T0_ERR_NOT_FOUND for a missing or unusable file; invalidate drops
+ * the file and the in-memory entry. */
+int t0_tuner_cache_store(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype,
+                         const t0_gemm_config* cfg, double tflops);
+int t0_tuner_cache_load(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype,
+                        t0_gemm_config* cfg, double* tflops);
+int t0_tuner_invalidate(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype);
 /* Replaces auto_gemm::auto_gemm (src/t0/auto_gemm.rs:555-590): tune then run
  * (NT, f32 out, like the reference). */
 int t0_auto_gemm(t0_runtime* rt, uint64_t a, uint64_t b, uint64_t c, uint32_t m, uint32_t n, uint32_t k,

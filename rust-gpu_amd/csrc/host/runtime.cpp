@@ -12,6 +12,7 @@
 #include <fstream>
 #include <map>
 #include <mutex>
+#include <set>
 #include <sstream>
 #include <string>
 #include <sys/stat.h>
@@ -51,6 +52,12 @@ struct t0_event {
     hipEvent_t ev = nullptr;
 };
 
+struct t0_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    t0_runtime* rt = nullptr;   // cleared when the runtime goes first
+};
+
 struct t0_runtime {
     int device = 0;
     hipStream_t own_stream = nullptr;
@@ -69,6 +76,9 @@ struct t0_runtime {
     uint32_t* sem = nullptr;
     size_t sem_count = 0;
     void* probe = nullptr;          // t0_gemm_clock_probe timestamps
+    // Graphs instantiated from this runtime's stream (their kernel arguments
+    // hold ws / stage / sem, so those buffers must not move while any exists).
+    std::set<struct t0_graph*> graphs;
     // Held for the host side of every call that uses ws / stage / sem, so
     // that threads sharing the runtime never resize a buffer another call
     // has just put into its kernel arguments (recursive: calls nest).
@@ -113,8 +123,24 @@ int launch(t0_runtime* rt, hipFunction_t f, uint32_t gx, uint32_t gy, uint32_t g
     return T0_OK;
 }
 
+// A shared buffer may grow only outside graph capture (growing syncs the
+// stream, and the semaphores are cleared by a memset) and, once it exists,
+// only while no captured graph holds its address.
+int may_grow(t0_runtime* rt, const void* cur, const char* what) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(rt->stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone)
+        return fail(T0_ERR_INVALID, "the %s would grow during graph capture: run the same call once before capturing",
+                    what);
+    if (cur && !rt->graphs.empty())
+        return fail(T0_ERR_INVALID, "the %s would grow while %zu captured graph(s) hold its address: destroy them "
+                    "first, or run the largest call once before capturing", what, rt->graphs.size());
+    return T0_OK;
+}
+
 int ensure_ws(t0_runtime* rt, size_t bytes) {
     if (bytes <= rt->ws_bytes) return T0_OK;
+    int r = may_grow(rt, rt->ws, "split-K workspace");
+    if (r) return r;
     if (rt->ws) { HIPCHK(hipStreamSynchronize(rt->stream)); HIPCHK(hipFree(rt->ws)); rt->ws = nullptr; rt->ws_bytes = 0; }
     size_t want = std::max<size_t>(bytes + 4096, 64u << 20);
     HIPCHK(hipMalloc(&rt->ws, want));
@@ -124,6 +150,8 @@ int ensure_ws(t0_runtime* rt, size_t bytes) {
 
 int ensure_stage(t0_runtime* rt, size_t bytes) {
     if (bytes <= rt->stage_bytes) return T0_OK;
+    int r = may_grow(rt, rt->stage, "operand staging buffer");
+    if (r) return r;
     if (rt->stage) { HIPCHK(hipStreamSynchronize(rt->stream)); HIPCHK(hipFree(rt->stage)); rt->stage = nullptr; rt->stage_bytes = 0; }
     size_t want = std::max<size_t>(bytes + 4096, 16u << 20);
     HIPCHK(hipMalloc(&rt->stage, want));
@@ -133,6 +161,8 @@ int ensure_stage(t0_runtime* rt, size_t bytes) {
 
 int ensure_sem(t0_runtime* rt, size_t count) {
     if (count <= rt->sem_count) return T0_OK;
+    int r = may_grow(rt, rt->sem, "split-K semaphore array");
+    if (r) return r;
     if (rt->sem) { HIPCHK(hipStreamSynchronize(rt->stream)); HIPCHK(hipFree(rt->sem)); rt->sem = nullptr; rt->sem_count = 0; }
     size_t want = std::max<size_t>(count, 65536);
     HIPCHK(hipMalloc(&rt->sem, want * 4));
@@ -214,43 +244,123 @@ std::string cache_dir() {
     return std::string(home ? home : "/tmp") + "/.t0_autotune";   // src/t0/auto_gemm.rs:594-600
 }
 
-std::string tune_key(const t0_runtime* rt, uint32_t m, uint32_t n, uint32_t k, uint32_t tr, uint32_t od) {
+std::string tune_key_arch(const char* arch, uint32_t m, uint32_t n, uint32_t k, uint32_t tr, uint32_t od) {
     char b[160];
-    snprintf(b, sizeof b, "%s_%ux%ux%u_%s_%s", rt->arch.c_str(), m, n, k, tr == T0_NN ? "nn" : "nt",
+    snprintf(b, sizeof b, "%s_%ux%ux%u_%s_%s", arch, m, n, k, tr == T0_NN ? "nn" : "nt",
              od == T0_OUT_BF16 ? "bf16" : "f32");
     return b;
 }
+std::string tune_key(const t0_runtime* rt, uint32_t m, uint32_t n, uint32_t k, uint32_t tr, uint32_t od) {
+    return tune_key_arch(rt->arch.c_str(), m, n, k, tr, od);
+}
 
-bool load_cache(const std::string& key, t0_gemm_config* cfg, double* tf) {
-    std::ifstream f(cache_dir() + "/gemm_" + key + ".json");
+// Tuned configs on disk, one JSON file per problem in the reference's layout
+// (src/t0/auto_gemm.rs:435-501): tile_m, tile_n, tile_k, wg_size, split_k,
+// lds_pad, n_col_passes, wgp, swap, tflops, all.  NT with f32 output (the
+// reference's only form) keeps its file name gemm_MxNxK.json, so reference
+// cache files load; NN or bf16 output add a _nn / _nt and _bf16 / _f32
+// suffix.  Files written here also name the architecture ("arch") and the
+// layout; a file for another architecture is ignored.
+std::string cache_file(uint32_t m, uint32_t n, uint32_t k, uint32_t tr, uint32_t od) {
+    std::string f = "gemm_" + std::to_string(m) + "x" + std::to_string(n) + "x" + std::to_string(k);
+    if (tr != T0_NT || od != T0_OUT_F32)
+        f += std::string(tr == T0_NN ? "_nn" : "_nt") + (od == T0_OUT_BF16 ? "_bf16" : "_f32");
+    return cache_dir() + "/" + f + ".json";
+}
+
+// n values ~ N(0,1) rounded to bf16 (RNE): xorshift64* uniforms, Box-Muller
+void fill_normal_bf16(uint16_t* out, size_t n, uint64_t seed) {
+    uint64_t x = seed ? seed : 1;
+    auto uni = [&]() {   // (0, 1]
+        x ^= x >> 12; x ^= x << 25; x ^= x >> 27;
+        return ((x * 0x2545F4914F6CDD1Dull) >> 11) * (1.0 / 9007199254740992.0) + 1.0 / 18014398509481984.0;
+    };
+    auto rne = [](float f) {
+        uint32_t u;
+        memcpy(&u, &f, 4);
+        return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+    };
+    for (size_t i = 0; i < n; i += 2) {
+        const double r = std::sqrt(-2.0 * std::log(uni())), t = 6.283185307179586 * uni();
+        out[i] = rne((float)(r * std::cos(t)));
+        if (i + 1 < n) out[i + 1] = rne((float)(r * std::sin(t)));
+    }
+}
+
+// a config read back from disk is used only if a gfx950 kernel runs it
+bool tuned_config_ok(const t0_gemm_config& c) {
+    const uint32_t sk = split_of(c);
+    return instance_for(c) != nullptr && sk <= 16 && (sk & (sk - 1)) == 0 && c.transpose <= T0_NN &&
+           c.out_dtype <= T0_OUT_BF16;
+}
+
+bool load_cache_file(uint32_t m, uint32_t n, uint32_t k, uint32_t tr, uint32_t od, const char* arch,
+                     t0_gemm_config* cfg, double* tf) {
+    std::ifstream f(cache_file(m, n, k, tr, od));
     if (!f) return false;
     std::stringstream ss;
     ss << f.rdbuf();
     const std::string s = ss.str();
-    auto field = [&](const char* name) -> std::string {
-        std::string pat = std::string("\"") + name + "\":";
+    auto raw = [&](const char* name, std::string* out) {
+        const std::string pat = std::string("\"") + name + "\":";
         size_t p = s.find(pat);
-        if (p == std::string::npos) return "";
+        if (p == std::string::npos) return false;
         p += pat.size();
         while (p < s.size() && (s[p] == ' ' || s[p] == '"')) p++;
         size_t e = p;
         while (e < s.size() && s[e] != '"' && s[e] != ',' && s[e] != '}') e++;
-        return s.substr(p, e - p);
+        *out = s.substr(p, e - p);
+        return true;
     };
-    if (field("version") != "1") return false;
-    const std::string name = field("name");
-    if (name.empty() || t0_config_from_name(name.c_str(), cfg) != T0_OK) return false;
-    *tf = atof(field("tflops").c_str());
-    return t0_config_is_feasible(cfg) || (cfg->split_k > 1);
+    auto num = [&](const char* name, double* v) {
+        std::string t;
+        if (!raw(name, &t) || t.empty()) return false;
+        char* end = nullptr;
+        *v = strtod(t.c_str(), &end);
+        return end && *end == 0;
+    };
+    std::string a;
+    if (raw("arch", &a) && a != arch) return false;
+    double tm, tn, tk, wg, t;
+    if (!num("tile_m", &tm) || !num("tile_n", &tn) || !num("tile_k", &tk) || !num("wg_size", &wg) || !num("tflops", &t))
+        return false;
+    double sk = 1, pad = 0, passes = 1;
+    num("split_k", &sk);
+    num("lds_pad", &pad);
+    num("n_col_passes", &passes);
+    t0_gemm_config c;
+    memset(&c, 0, sizeof c);
+    c.tile_m = (uint32_t)tm; c.tile_n = (uint32_t)tn; c.tile_k = (uint32_t)tk; c.wg_size = (uint32_t)wg;
+    c.split_k = sk > 1 ? (uint32_t)sk : 0;
+    c.lds_pad = (uint32_t)pad;
+    c.n_col_passes = passes >= 1 ? (uint32_t)passes : 1;
+    c.use_lds = 1; c.double_buffer = 1;
+    c.wgp_mode = s.find("\"wgp\":true") != std::string::npos;
+    c.swap_grid = s.find("\"swap\":true") != std::string::npos;
+    c.transpose = (uint8_t)tr;
+    c.out_dtype = (uint8_t)od;
+    c.epilogue = T0_EPI_STORE_F32;
+    if (!tuned_config_ok(c)) return false;
+    *cfg = c;
+    *tf = t;
+    return true;
 }
 
-void save_cache(const std::string& key, const t0_gemm_config& cfg, double tf) {
+bool save_cache_file(uint32_t m, uint32_t n, uint32_t k, uint32_t tr, uint32_t od, const char* arch,
+                     const t0_gemm_config& c, double tf) {
     const std::string d = cache_dir();
     mkdir(d.c_str(), 0755);
-    std::ofstream f(d + "/gemm_" + key + ".json");
-    if (!f) return;
-    f << "{\"version\": \"1\", \"key\": \"" << key << "\", \"name\": \"" << config_name(cfg) << "\", \"tflops\": "
-      << tf << "}\n";
+    std::ofstream f(cache_file(m, n, k, tr, od));
+    if (!f) return false;
+    char num[32];
+    snprintf(num, sizeof num, "%.2f", tf);
+    f << "{\"tile_m\":" << c.tile_m << ",\"tile_n\":" << c.tile_n << ",\"tile_k\":" << c.tile_k
+      << ",\"wg_size\":" << c.wg_size << ",\"split_k\":" << split_of(c) << ",\"lds_pad\":" << c.lds_pad
+      << ",\"n_col_passes\":" << (c.n_col_passes ? c.n_col_passes : 1) << ",\"wgp\":" << (c.wgp_mode ? "true" : "false")
+      << ",\"swap\":" << (c.swap_grid ? "true" : "false") << ",\"tflops\":" << num << ",\"all\":[]"
+      << ",\"arch\":\"" << arch << "\",\"transpose\":\"" << (tr == T0_NN ? "nn" : "nt") << "\",\"out_dtype\":\""
+      << (od == T0_OUT_BF16 ? "bf16" : "f32") << "\",\"name\":\"" << config_name(c) << "\"}\n";
+    return (bool)f;
 }
 
 }  // namespace
@@ -291,6 +401,7 @@ int t0_runtime_destroy(t0_runtime* rt) {
     if (!rt) return T0_OK;
     hipSetDevice(rt->device);
     hipStreamSynchronize(rt->stream);
+    for (auto* g : rt->graphs) g->rt = nullptr;   // graphs outliving the runtime no longer point at it
     for (auto& kv : rt->cache) {
         if (kv.second->own_module) hipModuleUnload(kv.second->own_module);
         delete kv.second;
@@ -388,9 +499,12 @@ int t0_kernel_load(t0_runtime* rt, const void* co, size_t size, const char* symb
 int t0_ensure_kernel(t0_runtime* rt, const t0_gemm_config* cfg, t0_kernel** out) {
     if (!rt || !cfg || !out) return fail(T0_ERR_INVALID, "null argument");
     const std::string name = config_name(*cfg);
+    // the name format carries no wave count; tiles with several wave layouts
+    // (256x256x64 on 4 or 8 waves) are distinct kernels
+    const std::string key = name + "#w" + std::to_string(cfg->wg_size / 64);
     {
         std::lock_guard<std::mutex> g(rt->mu);
-        auto it = rt->cache.find(name);
+        auto it = rt->cache.find(key);
         if (it != rt->cache.end()) { *out = it->second; return T0_OK; }
     }
     std::string why;
@@ -408,7 +522,9 @@ int t0_ensure_kernel(t0_runtime* rt, const t0_gemm_config* cfg, t0_kernel** out)
     r = get_fn(rt, k->inst->symbol(cfg->transpose == T0_NN), &k->fn);
     if (r) { delete k; return r; }
     std::lock_guard<std::mutex> g(rt->mu);
-    rt->cache[name] = k;
+    auto it = rt->cache.find(key);
+    if (it != rt->cache.end()) { delete k; *out = it->second; return T0_OK; }   // another thread won
+    rt->cache[key] = k;
     *out = k;
     return T0_OK;
 }
@@ -416,13 +532,14 @@ int t0_ensure_kernel(t0_runtime* rt, const t0_gemm_config* cfg, t0_kernel** out)
 int t0_ensure_tile_kernel(t0_runtime* rt, const t0_tile_gemm* spec, t0_kernel** out) {
     if (!rt || !spec || !out) return fail(T0_ERR_INVALID, "null argument");
     const std::string name = tile_name(*spec);
-    {
-        std::lock_guard<std::mutex> g(rt->mu);
-        auto it = rt->cache.find(name);
-        if (it != rt->cache.end()) { *out = it->second; return T0_OK; }
-    }
     const GemmInstance* inst = tile_instance(*spec);
     if (!inst) return fail(T0_ERR_INFEASIBLE, "%s: no gfx950 kernel for this tile", name.c_str());
+    const std::string key = name + "#w" + std::to_string(inst->nw());
+    {
+        std::lock_guard<std::mutex> g(rt->mu);
+        auto it = rt->cache.find(key);
+        if (it != rt->cache.end()) { *out = it->second; return T0_OK; }
+    }
     if (spec->split_k > 1 && (spec->out_dtype == T0_OUT_BF16 || spec->n_epilogue))
         return fail(T0_ERR_INFEASIBLE, "%s: split-K planes must be f32 without epilogue", name.c_str());
     int r = set_dev(rt);
@@ -439,7 +556,9 @@ int t0_ensure_tile_kernel(t0_runtime* rt, const t0_tile_gemm* spec, t0_kernel** 
     r = get_fn(rt, inst->symbol(spec->transpose == T0_NN), &k->fn);
     if (r) { delete k; return r; }
     std::lock_guard<std::mutex> g(rt->mu);
-    rt->cache[name] = k;
+    auto it = rt->cache.find(key);
+    if (it != rt->cache.end()) { delete k; *out = it->second; return T0_OK; }
+    rt->cache[key] = k;
     *out = k;
     return T0_OK;
 }
@@ -448,7 +567,13 @@ int t0_get_kernel(t0_runtime* rt, const char* name, t0_kernel** out) {
     if (!rt || !name || !out) return fail(T0_ERR_INVALID, "null argument");
     std::lock_guard<std::mutex> g(rt->mu);
     auto it = rt->cache.find(name);
-    if (it == rt->cache.end()) return fail(T0_ERR_NOT_FOUND, "kernel %s not loaded", name);
+    if (it == rt->cache.end()) {
+        // GEMM kernels are cached as "<name>#w<waves>": the lowest wave count loaded under this name
+        const std::string pre = std::string(name) + "#w";
+        it = rt->cache.lower_bound(pre);
+        if (it == rt->cache.end() || it->first.compare(0, pre.size(), pre) != 0)
+            return fail(T0_ERR_NOT_FOUND, "kernel %s not loaded", name);
+    }
     *out = it->second;
     return T0_OK;
 }
@@ -667,10 +792,6 @@ int t0_event_elapsed_ms(const t0_event* a, const t0_event* b, float* ms) {
 }
 
 // ----------------------------------------------------------------- graphs --
-struct t0_graph {
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t exec = nullptr;
-};
 
 int t0_graph_begin(t0_runtime* rt) {
     if (!rt) return fail(T0_ERR_INVALID, "null runtime");
@@ -691,6 +812,11 @@ int t0_graph_end(t0_runtime* rt, t0_graph** out) {
         delete g;
         return fail(T0_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
     }
+    {
+        std::lock_guard<std::recursive_mutex> lk(rt->call_mu);
+        g->rt = rt;
+        rt->graphs.insert(g);
+    }
     *out = g;
     return T0_OK;
 }
@@ -704,6 +830,10 @@ int t0_graph_launch(t0_runtime* rt, const t0_graph* g) {
 
 int t0_graph_destroy(t0_graph* g) {
     if (!g) return T0_OK;
+    if (g->rt) {
+        std::lock_guard<std::recursive_mutex> lk(g->rt->call_mu);
+        g->rt->graphs.erase(g);
+    }
     if (g->exec) hipGraphExecDestroy(g->exec);
     if (g->graph) hipGraphDestroy(g->graph);
     delete g;
@@ -749,7 +879,7 @@ int t0_gemm_select(t0_runtime* rt, const t0_gemm_desc* d, t0_gemm_config* out) {
         if (it != T.mem.end()) { *out = it->second.first; return T0_OK; }
     }
     double tf;
-    if (load_cache(key, out, &tf)) {
+    if (load_cache_file(d->m, d->n, d->k, d->transpose, d->out_dtype, rt->arch.c_str(), out, &tf)) {
         std::lock_guard<std::mutex> g(T.mu);
         T.mem[key] = {*out, tf};
         return T0_OK;
@@ -844,6 +974,36 @@ int t0_tuner_set_params(uint32_t max_candidates, uint32_t n_iters) {
     return T0_OK;
 }
 
+// The tuning cache on disk without a runtime (gfx950 entries): warm-start a
+// tuner with known picks, read one back, or drop one
+// (src/t0/auto_gemm.rs:439-507: load_cache, save_cache, invalidate).
+int t0_tuner_cache_store(uint32_t m, uint32_t n, uint32_t k, uint32_t tr, uint32_t od, const t0_gemm_config* cfg,
+                         double tflops) {
+    if (!cfg || !m || !n || !k || tr > T0_NN || od > T0_OUT_BF16) return fail(T0_ERR_INVALID, "bad arguments");
+    if (!tuned_config_ok(*cfg)) return fail(T0_ERR_INFEASIBLE, "%s: no gfx950 kernel", config_name(*cfg).c_str());
+    std::lock_guard<std::mutex> g(tuner().mu);
+    if (!save_cache_file(m, n, k, tr, od, "gfx950", *cfg, tflops))
+        return fail(T0_ERR_INVALID, "cannot write %s", cache_file(m, n, k, tr, od).c_str());
+    tuner().mem.erase(tune_key_arch("gfx950", m, n, k, tr, od));
+    return T0_OK;
+}
+
+int t0_tuner_cache_load(uint32_t m, uint32_t n, uint32_t k, uint32_t tr, uint32_t od, t0_gemm_config* cfg,
+                        double* tflops) {
+    if (!cfg || !tflops) return fail(T0_ERR_INVALID, "null output");
+    std::lock_guard<std::mutex> g(tuner().mu);
+    if (!load_cache_file(m, n, k, tr, od, "gfx950", cfg, tflops))
+        return fail(T0_ERR_NOT_FOUND, "no usable tuned config in %s", cache_file(m, n, k, tr, od).c_str());
+    return T0_OK;
+}
+
+int t0_tuner_invalidate(uint32_t m, uint32_t n, uint32_t k, uint32_t tr, uint32_t od) {
+    std::lock_guard<std::mutex> g(tuner().mu);
+    tuner().mem.erase(tune_key_arch("gfx950", m, n, k, tr, od));
+    remove(cache_file(m, n, k, tr, od).c_str());
+    return T0_OK;
+}
+
 // 256^3 smoke test of one candidate (src/t0/auto_gemm.rs:223-272): small
 // integer data (exact in bf16 and in the f32 sums) checked at sampled points
 // against the exact integer product.
@@ -913,7 +1073,7 @@ int t0_tune(t0_runtime* rt, uint32_t m, uint32_t n, uint32_t k, uint32_t tr, uin
     }
     t0_gemm_config cached;
     double tf = 0;
-    if (load_cache(key, &cached, &tf)) {
+    if (load_cache_file(m, n, k, tr, od, rt->arch.c_str(), &cached, &tf)) {
         std::lock_guard<std::mutex> g(T.mu);
         T.mem[key] = {cached, tf};
         if (cfg_out) *cfg_out = cached;
@@ -937,8 +1097,17 @@ int t0_tune(t0_runtime* rt, uint32_t m, uint32_t n, uint32_t k, uint32_t tr, uin
     HIPCHK(hipMalloc(&da, (size_t)m * k * 2));
     HIPCHK(hipMalloc(&db, (size_t)n * k * 2));
     HIPCHK(hipMalloc(&dc, (size_t)m * n * ob));
-    HIPCHK(hipMemset(da, 0x3c, (size_t)m * k * 2));
-    HIPCHK(hipMemset(db, 0x3c, (size_t)n * k * 2));
+    {
+        // seeded N(0,1) operands rounded to bf16: the MFMA clock under load
+        // depends on the data (constant operands run faster), so candidates are
+        // timed on data like the callers' (the reference zero-fills them,
+        // src/t0/auto_gemm.rs:311-314)
+        std::vector<uint16_t> h(std::max((size_t)m * k, (size_t)n * k));
+        fill_normal_bf16(h.data(), (size_t)m * k, 0x9E3779B97F4A7C15ull);
+        HIPCHK(hipMemcpy(da, h.data(), (size_t)m * k * 2, hipMemcpyHostToDevice));
+        fill_normal_bf16(h.data(), (size_t)n * k, 0xD1B54A32D192ED03ull);
+        HIPCHK(hipMemcpy(db, h.data(), (size_t)n * k * 2, hipMemcpyHostToDevice));
+    }
     t0_gemm_desc d;
     memset(&d, 0, sizeof d);
     d.a = (uint64_t)da; d.b = (uint64_t)db; d.c = (uint64_t)dc;
@@ -981,7 +1150,7 @@ int t0_tune(t0_runtime* rt, uint32_t m, uint32_t n, uint32_t k, uint32_t tr, uin
         tf = 0;
     } else {
         tf = 2.0 * m * n * k / (best_us * 1e-6) / 1e12;
-        save_cache(key, best, tf);
+        save_cache_file(m, n, k, tr, od, rt->arch.c_str(), best, tf);
     }
     {
         std::lock_guard<std::mutex> g(T.mu);

@@ -524,6 +524,26 @@ class GemmTuner:
         _check(lib().t0_tune(rt.h, m, n, k, transpose, out_dtype, C.byref(c), C.byref(tf)))
         return c, tf.value
 
+    @staticmethod
+    def save_cache(m: int, n: int, k: int, cfg: GemmConfig, tflops: float, transpose=NT, out_dtype=OUT_F32):
+        """GemmTuner::save_cache (src/t0/auto_gemm.rs:474-501)."""
+        _check(lib().t0_tuner_cache_store(m, n, k, transpose, out_dtype, C.byref(cfg), tflops))
+
+    @staticmethod
+    def load_cache(m: int, n: int, k: int, transpose=NT, out_dtype=OUT_F32):
+        """GemmTuner::load_cache (src/t0/auto_gemm.rs:439-472): (config, tflops) or None."""
+        c, tf = GemmConfig(), C.c_double()
+        rc = lib().t0_tuner_cache_load(m, n, k, transpose, out_dtype, C.byref(c), C.byref(tf))
+        if rc == -6:   # T0_ERR_NOT_FOUND
+            return None
+        _check(rc)
+        return c, tf.value
+
+    @staticmethod
+    def invalidate(m: int, n: int, k: int, transpose=NT, out_dtype=OUT_F32):
+        """GemmTuner::invalidate (src/t0/auto_gemm.rs:503-507)."""
+        _check(lib().t0_tuner_invalidate(m, n, k, transpose, out_dtype))
+
 
 def auto_gemm(rt: GpuRuntime, a: int, b: int, c: int, m: int, n: int, k: int) -> float:
     tf = C.c_double()

@@ -1,7 +1,8 @@
 """Helpers for the GPU parity tests: data generation through the oracle's
-bf16 rounding, device round trips, and the acceptance tolerance
-max|err| <= 1e-2 * sqrt(K) * max|a| * max|b| (relative Frobenius error is
-reported alongside)."""
+bf16 rounding, device round trips, BASELINE's acceptance tolerance
+max|err| <= 1e-2 * sqrt(K) * max|a| * max|b|, and the tight per-element bound
+of parity.tight_bound (f32 summation in any order, plus half a bf16 ulp for
+bf16 output) with the relative Frobenius error."""
 import numpy as np
 
 import t0_gpu as t0
@@ -18,6 +19,23 @@ def f32(h) -> np.ndarray:
 
 def tolerance(a_vals: np.ndarray, b_vals: np.ndarray, k: int) -> float:
     return 1e-2 * np.sqrt(k) * float(np.abs(a_vals).max()) * float(np.abs(b_vals).max()) + 1e-30
+
+
+def check_tight(got: np.ndarray, ref: np.ndarray, a_vals: np.ndarray, b_vals: np.ndarray, out_bf16: bool,
+                what: str = "", layout: str = "nn"):
+    """Per-element tight bound (parity.tight_bound) and, for bf16 output,
+    relative Frobenius error <= 2^-8; returns (max|err|, rel frob)."""
+    from oracle.parity import tight_bound, rel_frobenius
+    bound = tight_bound(ref, a_vals, b_vals, out_bf16, layout)
+    err = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+    frob = rel_frobenius(got, ref)
+    assert np.all(np.isfinite(got)), f"{what}: non-finite output"
+    bad = err > bound
+    assert not bad.any(), (f"{what}: {int(bad.sum())} outputs over the tight bound, worst excess "
+                           f"{float((err - bound).max()):.3e} (max|err| {float(err.max()):.3e}, rel frob {frob:.3e})")
+    if out_bf16:
+        assert frob <= 2.0 ** -8, f"{what}: rel frob {frob:.3e} > 2^-8"
+    return float(err.max()), frob
 
 
 def check_close(got: np.ndarray, ref: np.ndarray, tol: float, what: str = ""):

@@ -288,3 +288,63 @@ def test_gptq_rejects_out_of_range_zero_point():
     raw = _gptq_fixture(zp=16)
     with pytest.raises(t0.T0Error):
         t0.GptqWeight.from_bytes(raw).to_w4a16()
+
+
+# ----------------------------------------------------- tuning cache on disk --
+
+def _cfg_fields(c):
+    return {f: getattr(c, f) for f, _ in t0.GemmConfig._fields_ if f != "reserved"}
+
+
+def test_tuner_cache_roundtrip_keeps_wave_count(tmp_path):
+    """A pick saved to disk and loaded back (a new process reads only the
+    file) runs the same kernel: the 8-wave 256x256 instance that wins at
+    4096^3 shares its name with the 4-wave one, so the file carries wg_size
+    (src/t0/auto_gemm.rs:474-501 writes it too)."""
+    t0.lib().t0_tuner_set_cache_dir(str(tmp_path).encode())
+    try:
+        pick = t0.auto_select(4096, 4096, 4096)
+        assert pick.wg_size == 512
+        assert t0.GemmConfig.from_name(pick.name()).wg_size != pick.wg_size   # the name alone loses it
+        for tr, od in ((t0.NT, t0.OUT_F32), (t0.NN, t0.OUT_BF16)):
+            c = pick.copy(transpose=tr, out_dtype=od)
+            t0.GemmTuner.save_cache(4096, 4096, 4096, c, 1234.5, transpose=tr, out_dtype=od)
+            back, tf = t0.GemmTuner.load_cache(4096, 4096, 4096, transpose=tr, out_dtype=od)
+            assert _cfg_fields(back) == _cfg_fields(c) and tf == 1234.5
+        # the reference's file name for NT / f32, a suffixed one otherwise
+        assert (tmp_path / "gemm_4096x4096x4096.json").exists()
+        assert (tmp_path / "gemm_4096x4096x4096_nn_bf16.json").exists()
+        # a split-K pick round-trips too
+        sk = t0.auto_select(128, 4096, 4096)
+        t0.GemmTuner.save_cache(128, 4096, 4096, sk, 200.0)
+        back, _ = t0.GemmTuner.load_cache(128, 4096, 4096)
+        assert _cfg_fields(back) == _cfg_fields(sk)
+        t0.GemmTuner.invalidate(128, 4096, 4096)
+        assert t0.GemmTuner.load_cache(128, 4096, 4096) is None
+    finally:
+        t0.lib().t0_tuner_set_cache_dir(b"")
+
+
+def test_tuner_cache_reads_reference_files_and_rejects_unusable(tmp_path):
+    """A file in the reference's own format (no arch field) loads as an NT /
+    f32 config; a split_k the kernels cannot run, a tile without a gfx950
+    kernel, or another architecture's file is ignored (NOT_FOUND), so the
+    tuner ranks afresh instead of failing every later call."""
+    t0.lib().t0_tuner_set_cache_dir(str(tmp_path).encode())
+    try:
+        ref = ('{"tile_m":128,"tile_n":64,"tile_k":32,"wg_size":128,"split_k":2,"lds_pad":0,'
+               '"n_col_passes":1,"wgp":true,"swap":false,"tflops":79.20,"all":[["t0_gemm_128x64_k32_ldsdb",79.2]]}')
+        (tmp_path / "gemm_1024x1024x1024.json").write_text(ref)
+        c, tf = t0.GemmTuner.load_cache(1024, 1024, 1024)
+        assert (c.tile_m, c.tile_n, c.tile_k, c.wg_size, c.split_k, c.wgp_mode, c.swap_grid) == (128, 64, 32, 128, 2, 1, 0)
+        assert tf == pytest.approx(79.2) and c.transpose == t0.NT and c.out_dtype == t0.OUT_F32
+        for bad in (ref.replace('"split_k":2', '"split_k":3'), ref.replace('"split_k":2', '"split_k":32'),
+                    ref.replace('"tile_m":128', '"tile_m":96'), ref.replace('"wg_size":128', '"wg_size":192'),
+                    ref.replace('"tflops":79.20', '"tflops":"x"'), ref[:-1] + ',"arch":"gfx1100"}', "{}"):
+            (tmp_path / "gemm_1024x1024x1024.json").write_text(bad)
+            assert t0.GemmTuner.load_cache(1024, 1024, 1024) is None, bad
+        # storing a config no kernel runs is refused
+        with pytest.raises(t0.T0Error):
+            t0.GemmTuner.save_cache(64, 64, 64, t0.GemmConfig.tile_128x64_k16().copy(wg_size=192), 1.0)
+    finally:
+        t0.lib().t0_tuner_set_cache_dir(b"")

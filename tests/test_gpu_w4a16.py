@@ -6,6 +6,7 @@ import pytest
 
 import t0_gpu as t0
 from gpu_util import Dev, bf16, check_close, f32, tolerance
+from oracle.parity import rel_frobenius, w4_tight_bound
 from oracle import oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -125,19 +126,48 @@ def test_w4a16_decode_f32_scales(rt, dev):
     check_close(got, orc.w4a16(a, qw, s, None, 8, m, n, k, gs), w4_tol(a, qw, s, None, 8, n, k, gs), "f32 scales")
 
 
+def _w4_parts(qw, s, zw, zc, n, k, gs):
+    """[N][K] nibbles, [G][N] f32 scales and [G][N] zero points of a W4A16 operand."""
+    q = orc.int4_unpack(qw.view(np.uint8), n * k).reshape(n, k)
+    G = k // gs
+    if zw is None:
+        z = np.full((G, n), zc)
+    else:
+        z = np.zeros((G, n), np.int64)
+        for j in range(8):
+            z[:, j::8] = ((zw >> np.uint32(4 * j)) & 0xF).astype(np.int64)
+    return q, f32(s), z
+
+
+def check_w4_tight(got, ref, a, qw, s, zw, zc, n, k, gs, out_bf16, what):
+    q, sf, z = _w4_parts(qw, s, zw, zc, n, k, gs)
+    bound = w4_tight_bound(ref, f32(a), q, sf, z, gs, out_bf16)
+    err = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+    frob = rel_frobenius(got, ref)
+    assert np.all(err <= bound), (f"{what}: {int((err > bound).sum())} outputs over the tight bound "
+                                  f"(max|err| {float(err.max()):.3e}, rel frob {frob:.3e})")
+    if out_bf16:
+        assert frob <= 2.0 ** -8, f"{what}: rel frob {frob:.3e}"
+    print(f"{what}: max|err| {float(err.max()):.4g}, rel frob {frob:.4g}")
+
+
 def test_w4a16_decode_headline(rt, dev):
     """The decode headline: A[16,4096] ~ N(0,1), W[4096,11008] int4, g=128,
-    bf16 scales ~U(0.005,0.02), z = 8; checked on a 1376-column block and
-    with an integer closed form over the whole matrix."""
+    bf16 scales ~U(0.005,0.02), z = 8; a 1376-column block against the
+    oracle under BASELINE's bound and the tight W4A16 bound, with bf16 and f32
+    output; and an integer closed form over the whole matrix."""
     rng = np.random.default_rng(44)
     m, n, k, gs = 16, 11008, 4096, 128
     qw, s, _ = make_w4(rng, n, k, gs, per_group_zeros=False)
     a = bf16(rng.standard_normal((m, k)))
-    got = run_w4(rt, dev, a, qw, s, None, m, n, k, gs)
     j0, j1 = 4096, 4096 + 1376
-    ref = orc.w4a16(a, qw[j0:j1].copy(), s[:, j0:j1].copy(), None, 8, m, j1 - j0, k, gs)
-    check_close(got[:, j0:j1], ref, w4_tol(a, qw[j0:j1].copy(), s[:, j0:j1].copy(), None, 8, j1 - j0, k, gs),
-                "decode 16x4096x11008")
+    qb, sb = qw[j0:j1].copy(), s[:, j0:j1].copy()
+    ref = orc.w4a16(a, qb, sb, None, 8, m, j1 - j0, k, gs)
+    for out_f32 in (False, True):
+        got = run_w4(rt, dev, a, qw, s, None, m, n, k, gs, out_f32=out_f32)
+        check_close(got[:, j0:j1], ref, w4_tol(a, qb, sb, None, 8, j1 - j0, k, gs), "decode 16x4096x11008")
+        check_w4_tight(got[:, j0:j1], ref, a, qb, sb, None, 8, j1 - j0, k, gs, not out_f32,
+                       f"decode 16x4096x11008 {'f32' if out_f32 else 'bf16'} out")
     # whole-matrix closed form: unit scales, integer activations -> exact integers
     ones = np.full_like(s, 0x3F80)
     ai = rng.integers(-2, 3, size=(m, k))
@@ -233,7 +263,8 @@ def test_w4a16_prefill_exact_integers(rt, dev, per_group_zeros):
 
 
 def test_w4a16_prefill_headline_rows(rt, dev):
-    """The prefill shape: 4096x4096x14336, per-group zero points; sampled rows."""
+    """The prefill shape: 4096x4096x14336, per-group zero points; sampled
+    rows under BASELINE's bound and the tight W4A16 bound."""
     rng = np.random.default_rng(45)
     m, n, k, gs = 4096, 14336, 4096, 128
     qw, s, zw = make_w4(rng, n, k, gs, per_group_zeros=True)
@@ -243,6 +274,7 @@ def test_w4a16_prefill_headline_rows(rt, dev):
     ref = np.concatenate([orc.w4a16(a, qw, s, zw, 0, m, n, k, gs, r, r + 1) for r in rows])
     check_close(got[rows], ref, w4_tol(a, qw[:2048].copy(), s[:, :2048].copy(), zw[:, :256].copy(), 0, 2048, k, gs),
                 "prefill rows")
+    check_w4_tight(got[rows], ref, a[rows], qw, s, zw, 0, n, k, gs, True, "prefill 4096x4096x14336 bf16 out")
 
 
 def test_w4a16_generic_group_64(rt, dev):
