@@ -309,6 +309,21 @@ int t0_gemm_select(t0_runtime* rt, const t0_gemm_desc* d, t0_gemm_config* out);
  * workgroups.  Synchronous. */
 int t0_gemm_clock_probe(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm_desc* d, double* sclk_mhz,
                         double* span_us);
+/* No counterpart in the reference: t0_gemm for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Same arguments and results as t0_gemm; the
+ * in-kernel split-K keeps its counters and partial tiles in a fixed
+ * per-device scratch array of T0_NOALLOC_SCRATCH_BYTES that the library holds
+ * until the process ends, instead of the runtime's growable workspace, and
+ * the call allocates and frees nothing.  Limits: at most
+ * T0_NOALLOC_MAX_TILES output tiles and split_k * tiles * tile_m * tile_n * 4
+ * <= T0_NOALLOC_SCRATCH_BYTES - 4 * T0_NOALLOC_MAX_TILES bytes of partials,
+ * else T0_ERR_INVALID (nothing launched).  The counters used are cleared at
+ * each call.  Every call on one GPU shares that GPU's array, so calls that
+ * overlap on one GPU (other streams, other threads) race. */
+#define T0_NOALLOC_SCRATCH_BYTES (32u << 20)
+#define T0_NOALLOC_MAX_TILES 16384u
+int t0_gemm_noalloc(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm_desc* d);
 
 /* Replaces auto_gemm::GemmTuner::tune (src/t0/auto_gemm.rs:82-216) and the
  * JSON cache (src/t0/auto_gemm.rs:435-501): benchmark candidate configs on

@@ -51,4 +51,16 @@ struct Candidate {
 std::vector<Candidate> rank_candidates(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose,
                                        uint32_t out_dtype, bool allow_fixup);
 
+// ---- GEMM on caller-provided scratch (the no-allocation entry point) -----------
+// Runs t0_gemm with the in-kernel split-K using `scratch` (device memory of
+// `bytes`): counters for up to T0_NOALLOC_MAX_TILES tiles first, partial tiles
+// after them.  Allocates nothing; clears the counters it uses with a kernel.
+int gemm_with_scratch(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm_desc* d, void* scratch,
+                      size_t bytes);
+int runtime_device(const t0_runtime* rt);
+
 }  // namespace t0h
+
+// Implemented in csrc/host/noalloc.hip (compiled by hipcc with its device
+// array): resolves that array's address on the current device.
+extern "C" int t0h_noalloc_setup(int device);

@@ -187,8 +187,14 @@ bool fast_ok(const t0_gemm_params& p, bool nn, bool b_cols_padded = false) {
     return true;
 }
 
+// Caller-provided split-K scratch (no allocation): counters then partials.
+struct Scratch {
+    void* base = nullptr;
+    size_t bytes = 0;
+};
+
 int run_gemm_params(t0_runtime* rt, const GemmInstance* g, bool nn, t0_gemm_params& p, uint32_t threads_override = 0,
-                    bool b_cols_padded = false) {
+                    bool b_cols_padded = false, const Scratch* sc = nullptr) {
     hipFunction_t f;
     if (!g || !fast_ok(p, nn, b_cols_padded)) {
         if (p.flags & T0_GEMM_FIXUP) {   // generic kernel writes planes; reduce separately
@@ -202,7 +208,24 @@ int run_gemm_params(t0_runtime* rt, const GemmInstance* g, bool nn, t0_gemm_para
     int r = get_fn(rt, g->symbol(nn), &f);
     if (r) return r;
     const uint32_t tiles = ((p.M + g->bm - 1) / g->bm) * ((p.N + g->bn - 1) / g->bn);
-    if (p.flags & T0_GEMM_FIXUP) {
+    if ((p.flags & T0_GEMM_FIXUP) && sc) {
+        const size_t partials = (size_t)p.split_k * tiles * g->bm * g->bn * 4;
+        if (tiles > T0_NOALLOC_MAX_TILES || partials > sc->bytes - T0_NOALLOC_MAX_TILES * 4)
+            return fail(T0_ERR_INVALID, "split-K scratch: %u tiles (at most %u) and %zu bytes of partial tiles "
+                        "(at most %zu) for %ux%ux%u split %u", tiles, (unsigned)T0_NOALLOC_MAX_TILES, partials,
+                        sc->bytes - T0_NOALLOC_MAX_TILES * 4, p.M, p.N, p.K, p.split_k);
+        hipFunction_t fill;
+        r = get_fn(rt, "t0k_fill_u32", &fill);
+        if (r) return r;
+        t0_aux_params z;
+        memset(&z, 0, sizeof z);
+        z.dst = sc->base;
+        z.m = tiles;
+        r = launch(rt, fill, (tiles + 255) / 256, 1, 1, 256, z);   // counters start at zero
+        if (r) return r;
+        p.semaphores = (uint32_t*)sc->base;
+        p.workspace = (float*)((uint8_t*)sc->base + T0_NOALLOC_MAX_TILES * 4);
+    } else if (p.flags & T0_GEMM_FIXUP) {
         r = ensure_ws(rt, (size_t)p.split_k * tiles * g->bm * g->bn * 4);
         if (r) return r;
         r = ensure_sem(rt, tiles);
@@ -392,6 +415,13 @@ int t0_runtime_create(int device_ordinal, t0_runtime** out) {
         hipStreamDestroy(rt->own_stream);
         delete rt;
         return fail(T0_ERR_HIP, "hipModuleLoadData(embedded gfx950 code object): %s", hipGetErrorString(e));
+    }
+    int r = t0h_noalloc_setup(device_ordinal);   // the no-allocation entry's scratch on this device
+    if (r) {
+        hipModuleUnload(rt->module);
+        hipStreamDestroy(rt->own_stream);
+        delete rt;
+        return r;
     }
     *out = rt;
     return T0_OK;
@@ -891,7 +921,7 @@ int t0_gemm_select(t0_runtime* rt, const t0_gemm_desc* d, t0_gemm_config* out) {
 }
 
 static int gemm_impl(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm_desc* d, uint64_t* clock_probe,
-                     uint32_t* workgroups) {
+                     uint32_t* workgroups, const Scratch* sc = nullptr) {
     if (!rt || !d) return fail(T0_ERR_INVALID, "null argument");
     std::lock_guard<std::recursive_mutex> call_lock(rt->call_mu);
     if (!d->m || !d->n || !d->k) return fail(T0_ERR_INVALID, "empty GEMM %ux%ux%u", d->m, d->n, d->k);
@@ -920,8 +950,23 @@ static int gemm_impl(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm_de
         p.clock_probe = clock_probe;
         *workgroups = wgs;
     }
-    return run_gemm_params(rt, g, d->transpose == T0_NN, p);
+    return run_gemm_params(rt, g, d->transpose == T0_NN, p, 0, false, sc);
 }
+
+}  // extern "C"
+
+int t0h::gemm_with_scratch(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm_desc* d, void* scratch,
+                           size_t bytes) {
+    if (!scratch || bytes <= T0_NOALLOC_MAX_TILES * 4) return fail(T0_ERR_INVALID, "no scratch");
+    Scratch sc;
+    sc.base = scratch;
+    sc.bytes = bytes;
+    return gemm_impl(rt, cfg, d, nullptr, nullptr, &sc);
+}
+
+int t0h::runtime_device(const t0_runtime* rt) { return rt ? rt->device : -1; }
+
+extern "C" {
 
 int t0_gemm(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm_desc* d) {
     return gemm_impl(rt, cfg, d, nullptr, nullptr);

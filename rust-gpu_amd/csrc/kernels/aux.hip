@@ -308,3 +308,10 @@ extern "C" __global__ void __launch_bounds__(256) t0k_copy_b128(const t0_aux_par
     const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < p.plane_stride) ((u32x4_t*)p.dst)[i] = ((const u32x4_t*)p.src)[i];
 }
+
+// dst[0 .. m) = planes (u32 words): clears the split-K counters of the
+// no-allocation GEMM entry (a kernel, not a memset, so it may be captured).
+extern "C" __global__ void __launch_bounds__(256) t0k_fill_u32(const t0_aux_params p) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < p.m) ((uint32_t*)p.dst)[i] = p.planes;
+}

@@ -389,6 +389,14 @@ class GpuRuntime:
             d.epilogue[i] = TEPI[op] if isinstance(op, str) else op
         _check(lib().t0_gemm(self.h, C.byref(cfg) if cfg is not None else None, C.byref(d)))
 
+    def gemm_noalloc(self, a: int, b: int, c: int, m: int, n: int, k: int, transpose=NT, out_dtype=OUT_F32,
+                     cfg: GemmConfig | None = None, lda=0, ldb=0, ldc=0):
+        """t0_gemm without device allocation: split-K partials and counters in
+        the library's fixed per-device scratch array (see t0_gemm_noalloc)."""
+        d = GemmDescC(a=a, b=b, c=c, m=m, n=n, k=k, lda=lda, ldb=ldb, ldc=ldc, transpose=transpose,
+                      out_dtype=out_dtype)
+        _check(lib().t0_gemm_noalloc(self.h, C.byref(cfg) if cfg is not None else None, C.byref(d)))
+
     def gemm_clock_probe(self, a: int, b: int, c: int, m: int, n: int, k: int, transpose=NT, out_dtype=OUT_F32,
                          cfg: GemmConfig | None = None):
         """One GEMM with per-workgroup timestamps: (median shader clock in MHz,
