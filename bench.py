@@ -120,6 +120,30 @@ def bench_copy(rt, steps, warmup, rng, tr):
             "us_per_launch": round(ms * 1e3, 3), "gbs": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}
 
 
+def bench_floor(rt, steps, warmup, rng, tr):
+    """Floors of the W4A16 decode (16x4096x11008): reading its 22.5 MB weight
+    array once (t0k_stream_read, 12 rotated copies so the Infinity Cache
+    cannot serve them) and an empty launch, for the decode's launch shape
+    (256 x 1024) and smaller workgroups; graph replays like the decode."""
+    n, k = 11008, 4096
+    wbytes = n * k // 2
+    sets = [rt.alloc(wbytes) for _ in range(ROTATE)]
+    for b in sets:
+        rt.memset(b.gpu_addr(), 0x5A, wbytes)
+    sink = rt.alloc(65536 * 4)
+    out = {"workload": "decode floors: read 22544384 B once / empty launch", "bytes": wbytes}
+    for wgs, thr in ((256, 1024), (256, 512), (256, 256), (512, 256), (1024, 256)):
+        ms_r, med_r = rotate_timed(rt, lambda i: rt.floor_stream_read(sets[i].gpu_addr(), wbytes, sink.gpu_addr(),
+                                                                       wgs, thr), steps, warmup)
+        ms_e, med_e = rotate_timed(rt, lambda i: rt.floor_empty(wgs, thr), steps, warmup)
+        out[f"{wgs}x{thr}"] = {"us_read": round(ms_r * 1e3, 3), "us_read_median": round(med_r * 1e3, 3),
+                               "gbs_read": round(wbytes / (ms_r * 1e-3) / 1e9, 1), "us_empty": round(ms_e * 1e3, 3),
+                               "us_empty_median": round(med_e * 1e3, 3)}
+    for b in sets + [sink]:
+        b.free()
+    return out
+
+
 def load_traffic():
     p = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(p):
@@ -437,7 +461,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="issue rotated launches directly (for tracers)")
-    ap.add_argument("--only", choices=["gemm4096", "skinny", "decode", "prefill", "ignis", "norm_decode", "copy"],
+    ap.add_argument("--only", choices=["gemm4096", "skinny", "decode", "prefill", "ignis", "norm_decode", "copy",
+                                       "floor"],
                     default=None,
                     help="run one workload (for counter collection)")
     args = ap.parse_args()
@@ -456,7 +481,7 @@ def main():
     if args.only:
         fn = {"gemm4096": bench_gemm_4096, "skinny": bench_skinny, "decode": bench_decode,
               "prefill": bench_prefill, "ignis": bench_ignis, "norm_decode": bench_norm_decode,
-              "copy": bench_copy}[args.only]
+              "copy": bench_copy, "floor": bench_floor}[args.only]
         r = fn(rt, args.steps, args.warmup, rng, tr)
         for key in ("a", "b", "_host"):
             r.pop(key, None)
@@ -469,8 +494,9 @@ def main():
           f"({head['kernel']})", file=sys.stderr, flush=True)
     extras = {}
     if not args.no_extras:
-        for name, fn in (("skinny", bench_skinny), ("w4a16_decode", bench_decode), ("w4a16_prefill", bench_prefill),
-                         ("ignis_matmul", bench_ignis), ("norm_decode", bench_norm_decode)):
+        for name, fn in (("skinny", bench_skinny), ("w4a16_decode", bench_decode), ("decode_floor", bench_floor),
+                         ("w4a16_prefill", bench_prefill), ("ignis_matmul", bench_ignis),
+                         ("norm_decode", bench_norm_decode)):
             extras[name] = fn(rt, args.steps, args.warmup, rng, tr)
             shown = {k: v for k, v in extras[name].items() if k != "_host"}
             print(f"# {name}: {json.dumps(shown)}", file=sys.stderr, flush=True)

@@ -410,6 +410,15 @@ int t0_f32_to_bf16(t0_runtime* rt, uint64_t src, uint64_t dst, uint64_t count);
 /* Device-to-device copy through a plain 16-byte-per-lane kernel (no
  * counterpart in the reference): the calibration kernel for HBM byte counters. */
 int t0_copy_device(t0_runtime* rt, uint64_t src, uint64_t dst, uint64_t bytes);
+/* Floors of the HBM-bound shapes (measurement aids, no reference
+ * counterpart): t0_floor_stream_read only reads `bytes` (16-byte aligned,
+ * < 4 GiB) with 16-byte loads on a grid of `workgroups` x `threads` (a
+ * multiple of 64, <= 1024) -- the time to stream a weight array once; sink
+ * takes at most workgroups * 4 bytes.  t0_floor_empty launches an empty
+ * kernel of that shape: the per-launch cost alone.  Asynchronous. */
+int t0_floor_stream_read(t0_runtime* rt, uint64_t src, uint64_t bytes, uint64_t sink, uint32_t workgroups,
+                         uint32_t threads);
+int t0_floor_empty(t0_runtime* rt, uint32_t workgroups, uint32_t threads);
 /* t0_unpad_2d (src/t0/math.rs): out[m][n] = padded[m][n_pad]. */
 int t0_unpad_2d(t0_runtime* rt, uint64_t padded, uint64_t out, uint32_t m, uint32_t n, uint32_t n_pad);
 

@@ -1351,7 +1351,7 @@ static int w4_plan(t0_runtime* rt, const t0_w4a16_desc* d, W4Plan& pl) {
         pl.bn = big ? 256 : 128;
         char b[64];
         // 128x256 tiles on 8 waves with three stages in LDS, 128x128 on 4
-        snprintf(b, sizeof b, big ? "t0k_w4a16_prefill_%ux%u_w2x4_s3" : "t0k_w4a16_prefill_%ux%u_w2x2_s2", pl.bm,
+        snprintf(b, sizeof b, big ? "t0k_w4a16_prefill_%ux%u_w1x8_s3" : "t0k_w4a16_prefill_%ux%u_w2x2_s2", pl.bm,
                  pl.bn);
         pl.sym = b;
         pl.gx = ((M + pl.bm - 1) / pl.bm) * ((N + pl.bn - 1) / pl.bn);
@@ -1480,6 +1480,37 @@ int t0_copy_device(t0_runtime* rt, uint64_t src, uint64_t dst, uint64_t bytes) {
     p.src = (const void*)src; p.dst = (void*)dst;
     p.plane_stride = bytes / 16;
     return launch(rt, f, (uint32_t)((bytes / 16 + 255) / 256), 1, 1, 256, p);
+}
+
+int t0_floor_stream_read(t0_runtime* rt, uint64_t src, uint64_t bytes, uint64_t sink, uint32_t workgroups,
+                         uint32_t threads) {
+    if (!rt || !src || !sink || bytes % 16 || src % 16 || bytes >= (1ull << 32))
+        return fail(T0_ERR_INVALID, "16-byte aligned source under 4 GiB and a sink of workgroups * 4 bytes");
+    if (!workgroups || !threads || threads % 64 || threads > 1024) return fail(T0_ERR_INVALID, "bad launch shape");
+    int r = set_dev(rt);
+    if (r) return r;
+    hipFunction_t f;
+    r = get_fn(rt, "t0k_stream_read", &f);
+    if (r) return r;
+    t0_aux_params p;
+    memset(&p, 0, sizeof p);
+    p.src = (const void*)src;
+    p.dst = (void*)sink;
+    p.plane_stride = bytes / 16;
+    p.m = 0x9E3779B9u;
+    return launch(rt, f, workgroups, 1, 1, threads, p);
+}
+
+int t0_floor_empty(t0_runtime* rt, uint32_t workgroups, uint32_t threads) {
+    if (!rt || !workgroups || !threads || threads % 64 || threads > 1024) return fail(T0_ERR_INVALID, "bad launch shape");
+    int r = set_dev(rt);
+    if (r) return r;
+    hipFunction_t f;
+    r = get_fn(rt, "t0k_empty", &f);
+    if (r) return r;
+    t0_aux_params p;
+    memset(&p, 0, sizeof p);
+    return launch(rt, f, workgroups, 1, 1, threads, p);
 }
 
 int t0_unpad_2d(t0_runtime* rt, uint64_t padded, uint64_t out, uint32_t m, uint32_t n, uint32_t n_pad) {

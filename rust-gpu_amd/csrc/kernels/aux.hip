@@ -315,3 +315,27 @@ extern "C" __global__ void __launch_bounds__(256) t0k_fill_u32(const t0_aux_para
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < p.m) ((uint32_t*)p.dst)[i] = p.planes;
 }
+
+// Floor calibration for the HBM-bound shapes.  t0k_stream_read reads
+// plane_stride 16-byte chunks of src (every lane one chunk per iteration,
+// grid-stride) and writes one word per workgroup only if the xor of
+// everything read equals m, a value the host never passes (so the loads
+// cannot be dropped and nothing else is written).  t0k_empty does nothing:
+// the per-launch cost of a grid of that shape.
+extern "C" __global__ void __launch_bounds__(1024) t0k_stream_read(const t0_aux_params p) {
+    const uint64_t n16 = p.plane_stride;
+    const uint64_t step = (uint64_t)gridDim.x * blockDim.x;
+    u32x4_t x = {0u, 0u, 0u, 0u};
+    const __amdgpu_buffer_rsrc_t r = t0::make_rsrc(p.src);
+    uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (; i + 3 * step < n16; i += 4 * step) {      // four 16-byte loads in flight per lane
+        const u32x4_t a = t0::buffer_load_x4(r, (uint32_t)(i * 16));
+        const u32x4_t b = t0::buffer_load_x4(r, (uint32_t)((i + step) * 16));
+        const u32x4_t c = t0::buffer_load_x4(r, (uint32_t)((i + 2 * step) * 16));
+        const u32x4_t d = t0::buffer_load_x4(r, (uint32_t)((i + 3 * step) * 16));
+        x ^= a ^ b ^ c ^ d;
+    }
+    for (; i < n16; i += step) x ^= t0::buffer_load_x4(r, (uint32_t)(i * 16));
+    if ((x[0] ^ x[1] ^ x[2] ^ x[3]) == p.m) ((uint32_t*)p.dst)[blockIdx.x] = 1u;
+}
+extern "C" __global__ void __launch_bounds__(1024) t0k_empty(const t0_aux_params p) {}

@@ -764,6 +764,7 @@ T0_W4_PREFILL(256, 128, 2, 2, 2)
 T0_W4_PREFILL(256, 128, 4, 2, 2)
 T0_W4_PREFILL(128, 128, 2, 2, 2)
 T0_W4_PREFILL(128, 256, 2, 4, 3)
+T0_W4_PREFILL(128, 256, 1, 8, 3)
 
 extern "C" __global__ void __launch_bounds__(256) t0k_w4a16_rowsum(const t0_w4a16_params p) { t0::w4_rowsum(p); }
 extern "C" __global__ void __launch_bounds__(256) t0k_w4a16_generic(const t0_w4a16_params p) { t0::w4_generic(p); }

@@ -455,6 +455,12 @@ class GpuRuntime:
         _check(lib().t0_graph_end(self.h, C.byref(g)))
         return Graph(self, g)
 
+    def floor_stream_read(self, src, nbytes, sink, workgroups=256, threads=1024):
+        _check(lib().t0_floor_stream_read(self.h, src, nbytes, sink, workgroups, threads))
+
+    def floor_empty(self, workgroups=256, threads=1024):
+        _check(lib().t0_floor_empty(self.h, workgroups, threads))
+
     def copy_device(self, src, dst, nbytes):
         _check(lib().t0_copy_device(self.h, src, dst, nbytes))
 

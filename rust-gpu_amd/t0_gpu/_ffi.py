@@ -146,6 +146,8 @@ SIGNATURES = {
     "t0_f32_to_bf16": ([vp, u64, u64, u64], C.c_int),
     "t0_unpad_2d": ([vp, u64, u64, u32, u32, u32], C.c_int),
     "t0_copy_device": ([vp, u64, u64, u64], C.c_int),
+    "t0_floor_stream_read": ([vp, u64, u64, u64, u32, u32], C.c_int),
+    "t0_floor_empty": ([vp, u32, u32], C.c_int),
     "t0_bf16_matmul": ([vp, u64, u64, u64, u32, u32, u32], C.c_int),
     "t0_bf16_matmul_backward_data": ([vp, u64, u64, u64, u32, u32, u32], C.c_int),
     "t0_bf16_matmul_backward_weight": ([vp, u64, u64, u64, u32, u32, u32], C.c_int),
