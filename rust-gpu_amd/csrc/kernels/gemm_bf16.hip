@@ -372,6 +372,115 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
         }
     };
 
+    // ---- ping-pong K loop (256 x 256 x 32, 8 waves, 4 stages) ---------------
+    // Waves 0-3 (rows 0-127) and 4-7 (rows 128-255) share the SIMDs in pairs
+    // (wave s and s + 4 on SIMD s) and run in opposite phases: in every
+    // phase one wave of each pair issues the 16 MFMAs of a 32-k stage from
+    // registers while the other reads its fragments of the next stage from
+    // LDS and issues its half of a later stage's DMA (waves 0-3 the A
+    // chunks, waves 4-7 the B chunks).  A barrier ends every phase, so no
+    // barrier ever finds both waves of a SIMD without MFMA work.
+    //   waves 0-3: LOAD(0) | COMPUTE(0) | LOAD(1) | COMPUTE(1) | ...
+    //   waves 4-7:   idle  |  LOAD(0)   | COMPUTE(0) | LOAD(1)  | ...
+    // Stage t lives in buffer t % 4; LOAD(i) issues stage i + 3 into the
+    // buffer of stage i - 1, which every wave finished reading (and waited
+    // for) before the barrier that precedes it.
+    // Measured at 4096^3: 112-117 us against 101-102 us for the two-stage
+    // 256 x 256 x 64 schedule on the same box.  With one reading wave per
+    // SIMD a LOAD phase takes ~700 cycles (16 fragment reads ~350, since the
+    // CU's LDS read rate drops to ~180 B/clk for b128 and ~105 B/clk for the
+    // transposing reads; 4 DMAs ~250 at the CU's 64 B/clk global->LDS rate)
+    // against the 16 MFMAs' ~520, so the MFMA pipes wait on the loads.
+    constexpr bool PP = BM == 256 && BN == 256 && BK == 32 && G::NW == 8 && STAGES == 4 && WM == 2;
+    uint64_t y_split_stride = 0;
+    if constexpr (PP) {
+        const bool is_y = wave >= 4;     // SGPR: uniform branches
+        constexpr int PPL = 4;           // DMA chunks per wave per stage (16 KB of A or of B over 4 waves)
+        static_assert(G::A_BYTES == PPL * 4 * 1024 && G::B_BYTES == PPL * 4 * 1024, "ping-pong DMA split");
+        uint32_t d_off[PPL], d_k[PPL], d_lds[PPL];
+#pragma unroll
+        for (int j = 0; j < PPL; j++) {
+            const uint32_t q = (wave & 3) * PPL + j;             // 1 KB chunk of the A or B tile
+            const uint32_t pos = q * 1024 + lane * 16;
+            if (!is_y) {
+                const uint32_t r = pos / (BK * 2), s = (pos % (BK * 2)) / 16;
+                const uint32_t c = s ^ swz_rows<G::CHA>(r);
+                d_off[j] = (m0 + r) < M ? r * lda * 2 + c * 16 : OOB_OFFSET;
+                d_k[j] = c * 8;
+                d_lds[j] = q * 1024;
+            } else if constexpr (NN) {
+                const uint32_t r = pos / (BN * 2), s = (pos % (BN * 2)) / 16;
+                const uint32_t c = s ^ swz_nn<G::CHB>(r);
+                d_off[j] = (n0 + c * 8) < N ? r * ldb * 2 + c * 16 : OOB_OFFSET;
+                d_k[j] = r;
+                d_lds[j] = G::A_BYTES + q * 1024;
+            } else {
+                const uint32_t r = pos / (BK * 2), s = (pos % (BK * 2)) / 16;
+                const uint32_t c = s ^ swz_rows<G::CHA>(r);
+                d_off[j] = (n0 + r) < N ? r * ldb * 2 + c * 16 : OOB_OFFSET;
+                d_k[j] = c * 8;
+                d_lds[j] = G::A_BYTES + q * 1024;
+            }
+        }
+        // this wave's PPL chunks of stage t (a K-tail stage masks per chunk,
+        // so every stage issues the same number of loads)
+        auto pp_issue = [&](uint32_t t) {
+            const uint32_t kt = t * BK;
+            const uint32_t st = lds_base + (t % STAGES) * G::STAGE_BYTES;
+            const bool tail = kt + BK > k_len;
+            const uint8_t* src = is_y ? (NN ? B0 + (size_t)kt * ldb * 2 : B0 + (size_t)kt * 2) : A0 + (size_t)kt * 2;
+            __amdgpu_buffer_rsrc_t r = make_rsrc(src);
+            if (!tail) {
+#pragma unroll
+                for (int j = 0; j < PPL; j++) dma_x4(r, __builtin_amdgcn_readfirstlane(st + d_lds[j]), d_off[j]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < PPL; j++)
+                    dma_x4(r, __builtin_amdgcn_readfirstlane(st + d_lds[j]), kt + d_k[j] >= k_len ? OOB_OFFSET : d_off[j]);
+            }
+        };
+        // at most `ahead` later stages of this wave's DMAs still in flight
+        auto pp_wait = [&](uint32_t ahead) {
+            if (ahead >= 2) wait_vmcnt_fence<2 * PPL>();
+            else if (ahead == 1) wait_vmcnt_fence<PPL>();
+            else wait_vmcnt_fence<0>();
+        };
+        auto pp_barrier = [&]() {
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        const uint32_t nh = nk;                          // 32-k stages
+#pragma unroll
+        for (uint32_t s = 0; s < 3; s++)
+            if (s < nh) pp_issue(s);
+        pp_wait(nh > 0 ? (nh - 1 < 2 ? nh - 1 : 2) : 0);   // stage 0 landed
+        y_split_stride = p.y_split_stride;
+        asm volatile("" : "+s"(y_split_stride));
+        pp_barrier();
+        if (is_y) pp_barrier();                          // waves 4-7 start one phase later
+        bf16x8_t pa[2][G::FM], pb[2][G::FN];
+        for (uint32_t i = 0; i < nh; i++) {
+            // LOAD(i): fragments of stage i, then this wave's share of stage i + 3
+            const LDS_AS uint8_t* sa = stage_ptr(i);
+            load_frags(sa, 0, pa[0], pb[0]);
+            load_frags(sa, 1, pa[1], pb[1]);
+            if (i + 3 < nh) pp_issue(i + 3);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            // stage i + 1 must have landed in every wave before the barrier
+            // that ends the phase after which waves 0-3 read it
+            const uint32_t ahead = nh - 1 > i + 1 ? (nh - 2 - i < 2 ? nh - 2 - i : 2) : 0;
+            if (is_y) pp_wait(ahead);
+            pp_barrier();
+            // COMPUTE(i)
+            mfmas(pa[0], pb[0]);
+            mfmas(pa[1], pb[1]);
+            if (!is_y) pp_wait(ahead);
+            if (!(is_y && i + 1 == nh)) pp_barrier();
+        }
+    }
+
+    if constexpr (!PP) {
     // prologue: every buffer, then stage 0 visible and its first fragments
 #pragma unroll
     for (int s = 0; s < STAGES; s++)
@@ -382,7 +491,7 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
     // barrier's wait: a scalar load still in flight at the K loop's entry
     // (the compiler hoists it there) turns the first LDS wait of every step
     // into a full one, since scalar loads complete out of order.
-    uint64_t y_split_stride = p.y_split_stride;
+    y_split_stride = p.y_split_stride;
     asm volatile("" : "+s"(y_split_stride));
     __syncthreads();
     bf16x8_t af[2][G::FM], bfr[2][G::FN];
@@ -443,6 +552,7 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
             }
         }
     }
+    }   // !PP
 
     // ---- epilogue -----------------------------------------------------------
     // acc[i][j][r] holds C[m0 + wm*TM + i*32 + lane%32][n0 + wn*TN + j*32 + 8*(r/4) + 4*(lane/32) + r%4].
@@ -450,7 +560,10 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
     // wave-private LDS region [32][TN + 4] f32 and written back row-major, so
     // global stores are full contiguous rows and the epilogue chain runs from
     // a compact loop.
-    __syncthreads();  // all waves are done reading the stage buffers
+    // all waves are done reading the stage buffers (the ping-pong loop's
+    // last barrier already ensures it: waves 0-3 stage their results while
+    // waves 4-7 issue their last MFMAs from registers)
+    if constexpr (!PP) __syncthreads();
     float* wreg = (float*)(smem) + wave * G::EPI_WAVE_FLOATS;
     uint8_t* Cb = (uint8_t*)p.C;
     const bool fixup = (p.flags & T0_GEMM_FIXUP) && sk > 1;

@@ -164,13 +164,14 @@ def test_64x64_four_wave_tile(rt, dev, m, n, k, split):
 
 
 @pytest.mark.parametrize("m,n,k", [(256, 256, 64), (300, 260, 128), (100, 700, 40), (256, 512, 200),
-                                   (513, 300, 1000), (256, 256, 4160)])
+                                   (513, 300, 1000), (256, 256, 4160), (64, 96, 24), (260, 300, 96)])
 def test_eight_wave_256_tiles(rt, dev, m, n, k):
     """The 8-wave 256x256 instances (BK 64 with two stages: the 4096^3
-    kernel; BK 32 with four), reached by explicit configs (512 threads):
-    one, two and many K steps, K tails, ragged M / N, NN and NT, f32 and
-    bf16 out. Small-integer operands keep every partial sum exact, so the
-    f32 output must match the integer product bit for bit."""
+    kernel; BK 32 with four stages and the ping-pong K loop), reached by
+    explicit configs (512 threads): one, two, three and many K steps, K
+    tails, ragged M / N, NN and NT, f32 and bf16 out. Small-integer operands
+    keep every partial sum exact, so the f32 output must match the integer
+    product bit for bit."""
     rng = np.random.default_rng(m * 3 + n + k)
     ai = rng.integers(-8, 9, size=(m, k))
     bi = rng.integers(-6, 7, size=(k, n))
@@ -303,6 +304,39 @@ def test_fixup_split_k_bf16_deterministic(rt, dev):
         g2 = run_gemm(rt, dev, a, b, m, n, k, t0.NN, t0.OUT_BF16, cfg=cfg)
         assert np.array_equal(g1.view(np.uint32), g2.view(np.uint32))
         check_close(g1, ref, tolerance(f32(a), f32(b), k), f"sk={sk}")
+
+
+@pytest.mark.parametrize("sk", [2, 4])
+def test_pingpong_tile_split_k(rt, dev, sk):
+    """The ping-pong 256x256x32 instance under split-K, bit-exact on
+    small-integer operands with ragged N and a K tail in each partition:
+    the in-kernel reduction (bf16 out, ragged M through t0_gemm), and f32
+    planes summed on the host through the gemm_gen dispatch, whose 40-byte
+    kernargs carry no M (the grid gives M / tile_m tiles, so M is a
+    multiple of 256 there, src/t0/gemm_gen.rs:308-329)."""
+    n, k = 520, 1120                          # K / split_k = 560 or 280: a partial last stage
+    rng = np.random.default_rng(sk)
+    base = t0.GemmConfig.tile_256x256_k32().copy(wg_size=512, split_k=sk)
+    for m, planes_path in ((300, False), (512, True)):
+        ai = rng.integers(-8, 9, size=(m, k))
+        bi = rng.integers(-6, 7, size=(k, n))
+        want = ai.astype(np.int64) @ bi.astype(np.int64)
+        a, b = bf16(ai), bf16(bi)
+        for layout, bb in ((t0.NN, b), (t0.NT, bf16(bi.T.copy()))):
+            if not planes_path:
+                got16 = run_gemm(rt, dev, a, bb, m, n, k, layout, t0.OUT_BF16,
+                                 cfg=base.copy(transpose=layout, out_dtype=t0.OUT_BF16))
+                assert np.array_equal(got16, f32(orc.bf16_rne(want.astype(np.float32)))), (sk, layout)
+                continue
+            cfg = base.copy(transpose=layout, out_dtype=t0.OUT_F32)
+            assert m % cfg.tile_m == 0
+            da, db = dev.up(a), dev.up(bb)
+            planes = dev.zeros(sk * m * n * 4)
+            kern = rt.ensure_kernel_t0(cfg)
+            gx, gy = t0.compute_grid_auto(cfg, m, n)
+            rt.dispatch(kern, [gx, gy, 1], t0.build_kernargs(da, db, planes, k, n, m, cfg))
+            p = dev.down(planes, np.float32, sk * m * n).reshape(sk, m, n)
+            assert np.array_equal(p.astype(np.int64).sum(axis=0), want), (sk, layout)
 
 
 def test_raw_kernel_load_and_dispatch(rt, dev):
