@@ -472,30 +472,42 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
     const uint32_t x_off2 = (1024 + lane * 16 < BM * 4 && m0 + 256 + lane * 4 < M) ? 1024 + lane * 16 : OOB_OFFSET;
     const uint32_t lds_base = (uint32_t)(uintptr_t)(LDS_AS uint8_t*)smem;
 
-    auto issue = [&](uint32_t t) {
+    // The q-th load of this wave for stage t: its A chunks, its W chunks,
+    // then (one wave each) the scales, the zero-point words and the row sums.
+    constexpr int NQ = G::A_LOADS + G::W_LOADS + 2;
+    auto issue_q = [&](uint32_t t, int q) {
         const uint32_t st = lds_base + (t % STAGES) * G::STAGE;
-        __amdgpu_buffer_rsrc_t ra = make_rsrc(A0 + (size_t)t * 256);
-        __amdgpu_buffer_rsrc_t rw = make_rsrc(W0 + (size_t)t * 64);
-#pragma unroll
-        for (int j = 0; j < G::A_LOADS; j++)
-            dma_x4(ra, __builtin_amdgcn_readfirstlane(st + (wave_s * G::A_LOADS + j) * 1024), a_off[j]);
-#pragma unroll
-        for (int j = 0; j < G::W_LOADS; j++)
-            dma_x4(rw, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + (wave_s * G::W_LOADS + j) * 1024), w_off[j]);
+        if (q < G::A_LOADS) {
+            dma_x4(make_rsrc(A0 + (size_t)t * 256), __builtin_amdgcn_readfirstlane(st + (wave_s * G::A_LOADS + q) * 1024),
+                   a_off[q]);
+            return;
+        }
+        q -= G::A_LOADS;
+        if (q < G::W_LOADS) {
+            dma_x4(make_rsrc(W0 + (size_t)t * 64),
+                   __builtin_amdgcn_readfirstlane(st + G::A_BYTES + (wave_s * G::W_LOADS + q) * 1024), w_off[q]);
+            return;
+        }
+        q -= G::W_LOADS;
         if (wave_s == 0) {
-            __amdgpu_buffer_rsrc_t rs = make_rsrc(S0 + (size_t)t * N * 4);
-            dma_x4(rs, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + G::W_BYTES), s_off);
+            if (q == 0)
+                dma_x4(make_rsrc(S0 + (size_t)t * N * 4), __builtin_amdgcn_readfirstlane(st + G::A_BYTES + G::W_BYTES),
+                       s_off);
         } else if (wave_s == 1) {
-            if (p.zeros) {
-                __amdgpu_buffer_rsrc_t rz = make_rsrc(p.zeros + (size_t)t * (N / 8) + n0 / 8);
-                dma_x1(rz, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + G::W_BYTES + G::Z_OFF), z_off);
-            }
+            if (q == 0 && p.zeros)
+                dma_x1(make_rsrc(p.zeros + (size_t)t * (N / 8) + n0 / 8),
+                       __builtin_amdgcn_readfirstlane(st + G::A_BYTES + G::W_BYTES + G::Z_OFF), z_off);
         } else if (wave_s == G::NW - 1) {
-            __amdgpu_buffer_rsrc_t rx = make_rsrc(X + (size_t)t * M + m0);
-            dma_x4(rx, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + G::W_BYTES + G::S_BYTES), x_off);
-            if constexpr (BM * 4 > 1024)
+            const __amdgpu_buffer_rsrc_t rx = make_rsrc(X + (size_t)t * M + m0);
+            if (q == 0)
+                dma_x4(rx, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + G::W_BYTES + G::S_BYTES), x_off);
+            else if (BM * 4 > 1024)
                 dma_x4(rx, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + G::W_BYTES + G::S_BYTES + 1024), x_off2);
         }
+    };
+    auto issue = [&](uint32_t t) {
+#pragma unroll
+        for (int q = 0; q < NQ; q++) issue_q(t, q);
     };
     f32x16_t acc[G::FM][G::FN];
 #pragma unroll
@@ -533,6 +545,125 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
     // scales at the start of the next step, under the first half's MFMAs.
     const bool late = G::NW >= 8 && ((wave >> 2) & 1);
 
+    // The correction block's operands from this lane's zero-point word and
+    // row sums: B column -(128 + z) in k 0..2 of lane half 0, A row R split
+    // hi/mid/lo (hi + mid + lo == R exactly) likewise.
+    auto zcol_of = [&](uint32_t zw, uint32_t col) {
+        const uint32_t z = p.zeros ? (zw >> (4 * (col % 8))) & 0xFu : p.zero_const;
+        const uint32_t zb = h ? 0u : 0xC300u + z;                     // bf16 -(128 + z)
+        return __builtin_bit_cast(bf16x8_t, u32x4_t{zb | (zb << 16), zb, 0u, 0u});
+    };
+    auto rrow_of = [&](float r) {
+        const uint32_t hi = __float_as_uint(r) & 0xFFFF0000u;
+        const float r1 = r - __uint_as_float(hi);                       // exact
+        const uint32_t mid = __float_as_uint(r1) & 0xFFFF0000u;
+        const uint32_t lo = __float_as_uint(r1 - __uint_as_float(mid)); // <= 8 significant bits: exact in bf16
+        return __builtin_bit_cast(bf16x8_t, u32x4_t{(hi >> 16) | mid, lo >> 16, 0u, 0u});
+    };
+
+    if constexpr (STAGES == 3) {
+        // One barrier per step, after its fourth 16-k sub-step: there every
+        // wave has finished step t - 1 (so stage t + 2 may go into its
+        // buffer, over sub-steps 4-7) and waits for its own loads of stage
+        // t + 1, which the barrier makes visible to all.  Sub-step 7 then
+        // reads step t + 1's first operands (A fragments, W words, zero-point
+        // word, row sums), so the step boundary has no barrier and no LDS
+        // wait, and the two waves of a SIMD drift apart instead of starting
+        // every step in the same phase.
+        constexpr int PER = (NQ + 3) / 4;
+        issue(0);
+        if (nk > 1) issue(1);
+        if (nk > 1) wait_vmcnt<G::MIN_LOADS>();
+        else wait_vmcnt<0>();
+        __syncthreads();
+        bf16x8_t af[2][G::FM];
+        u32x4_t wlo[G::FN], whi[G::FN], wlo_n[G::FN], whi_n[G::FN];
+        uint32_t zw[G::FN], zw_n[G::FN];
+        float xr[G::FM], xr_n[G::FM];
+        // step u's first operands, from stage u's buffer
+        auto read_first = [&](uint32_t u, bf16x8_t* a0, u32x4_t* wl, u32x4_t* wh, uint32_t* z, float* x) {
+            const LDS_AS uint8_t* st = (const LDS_AS uint8_t*)smem + (u % STAGES) * G::STAGE;
+            const LDS_AS uint32_t* sz = (const LDS_AS uint32_t*)(st + G::A_BYTES + G::W_BYTES + G::Z_OFF);
+            const LDS_AS float* sx = (const LDS_AS float*)(st + G::A_BYTES + G::W_BYTES + G::S_BYTES);
+#pragma unroll
+            for (int i = 0; i < G::FM; i++) {
+                a0[i] = *(const LDS_AS bf16x8_t*)(st + a_row0 + i * 32 * 256 + ((h * 8) ^ a_sw) * 16);
+                x[i] = h ? 0.0f : sx[wm * G::TM + i * 32 + l32];
+            }
+#pragma unroll
+            for (int j = 0; j < G::FN; j++) {
+                const uint32_t col = wn * G::TN + j * 32 + l32;
+                const LDS_AS uint8_t* wr = st + G::A_BYTES + col * 64;
+                wl[j] = *(const LDS_AS u32x4_t*)(wr + w_c0);
+                wh[j] = *(const LDS_AS u32x4_t*)(wr + w_c1);
+                z[j] = p.zeros ? sz[col / 8] : 0u;
+            }
+        };
+        if (nk) read_first(0, af[0], wlo, whi, zw, xr);
+        for (uint32_t t = 0; t < nk; t++) {
+            if (late && t > 0) scale_add();
+            const LDS_AS uint8_t* sa = (const LDS_AS uint8_t*)smem + (t % STAGES) * G::STAGE;
+            const LDS_AS float* ss = (const LDS_AS float*)(sa + G::A_BYTES + G::W_BYTES);
+#pragma unroll
+            for (int i = 0; i < G::FM; i++)
+#pragma unroll
+                for (int j = 0; j < G::FN; j++)
+                    tmp[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(zcol_of(zw[j], wn * G::TN + j * 32 + l32),
+                                                                        rrow_of(xr[i]), f32x16_t{}, 0, 0, 0);
+#pragma unroll
+            for (int kk = 0; kk < 8; kk++) {
+                const int cur = kk & 1;
+                if (kk == 4) {
+                    // A plain barrier: the LDS reads still in flight here are
+                    // of stage t, and every read of stage t - 1 (whose buffer
+                    // the DMA below refills) was consumed before this point.
+                    wait_vmcnt_fence<0>();   // this wave's loads of stage t + 1
+                    __builtin_amdgcn_sched_barrier(0);
+                    __builtin_amdgcn_s_barrier();
+                    __builtin_amdgcn_sched_barrier(0);
+                    asm volatile("" ::: "memory");
+                }
+                if (kk >= 4 && t + 2 < nk) {
+#pragma unroll
+                    for (int q = (kk - 4) * PER; q < (kk - 3) * PER && q < NQ; q++) issue_q(t + 2, q);
+                }
+                if (kk + 1 < 8) {
+#pragma unroll
+                    for (int i = 0; i < G::FM; i++) {
+                        const uint32_t c = (h * 8 + kk + 1) ^ a_sw;
+                        af[cur ^ 1][i] = *(const LDS_AS bf16x8_t*)(sa + a_row0 + i * 32 * 256 + c * 16);
+                    }
+                } else if (t + 1 < nk) {
+                    read_first(t + 1, af[cur ^ 1], wlo_n, whi_n, zw_n, xr_n);
+                }
+                // the next sub-step's reads stay ahead of this one's MFMAs
+                // (the scheduler would sink them next to their uses, into
+                // the same registers, and every sub-step would wait on them)
+                __builtin_amdgcn_sched_barrier(0);
+                bf16x8_t bw[G::FN];
+#pragma unroll
+                for (int j = 0; j < G::FN; j++) bw[j] = unpack8_128(kk < 4 ? wlo[j][kk] : whi[j][kk - 4], bits4300);
+#pragma unroll
+                for (int i = 0; i < G::FM; i++)
+#pragma unroll
+                    for (int j = 0; j < G::FN; j++)
+                        tmp[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[j], af[cur][i], tmp[i][j], 0, 0, 0);
+            }
+#pragma unroll
+            for (int j = 0; j < G::FN; j++) {
+#pragma unroll
+                for (int q4 = 0; q4 < 4; q4++)
+                    sv[j][q4] = *(const LDS_AS f32x4_t*)(ss + wn * G::TN + j * 32 + 8 * q4 + 4 * h);
+                wlo[j] = wlo_n[j];
+                whi[j] = whi_n[j];
+                zw[j] = zw_n[j];
+            }
+#pragma unroll
+            for (int i = 0; i < G::FM; i++) xr[i] = xr_n[i];
+            if (!late) scale_add();
+        }
+        if (late && nk) scale_add();
+    } else {
 #pragma unroll
     for (int s = 0; s < STAGES - 1; s++)
         if ((uint32_t)s < nk) issue(s);
@@ -613,6 +744,7 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
         if (!late) scale_add();
     }
     if (late && nk) scale_add();
+    }
 
     // epilogue: stage 32-row blocks through LDS, store rows
     __syncthreads();
