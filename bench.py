@@ -124,7 +124,8 @@ def bench_floor(rt, steps, warmup, rng, tr):
     """Floors of the W4A16 decode (16x4096x11008): reading its 22.5 MB weight
     array once (t0k_stream_read, 12 rotated copies so the Infinity Cache
     cannot serve them) and an empty launch, for the decode's launch shape
-    (256 x 1024) and smaller workgroups; graph replays like the decode."""
+    (256 x 1024) and smaller workgroups; graph replays like the decode.
+    Then the GEMM's ceilings (bench_ceilings)."""
     n, k = 11008, 4096
     wbytes = n * k // 2
     sets = [rt.alloc(wbytes) for _ in range(ROTATE)]
@@ -140,6 +141,49 @@ def bench_floor(rt, steps, warmup, rng, tr):
                                "gbs_read": round(wbytes / (ms_r * 1e-3) / 1e9, 1), "us_empty": round(ms_e * 1e3, 3),
                                "us_empty_median": round(med_e * 1e3, 3)}
     for b in sets + [sink]:
+        b.free()
+    out.update(bench_ceilings(rt, steps, warmup, rng))
+    return out
+
+
+def _clock_records(buf, wgs):
+    """(median shader MHz, median workgroup span in us, median workgroup
+    shader cycles) from the 4-u64 records of the floor kernels."""
+    r = buf.read(np.uint64, 4 * wgs).reshape(wgs, 4).astype(np.float64)
+    real, shader = r[:, 1] - r[:, 0], r[:, 3] - r[:, 2]
+    return float(np.median(shader / real * 100.0)), float(np.median(real / 100.0)), float(np.median(shader))
+
+
+def bench_ceilings(rt, steps, warmup, rng):
+    """Ceilings of the 4096^3 GEMM on this part: MFMA issue alone at the
+    8-wave 256x256 tile's count (2048 per wave, 4096 per SIMD = 131072
+    shader cycles) with N(0,1) bf16 operands and with zeros (the data sets
+    the power the MFMAs draw, hence the clock); and the LDS port rates per
+    CU (ds_read_b128, the NN operand's ds_read_b64_tr_b16, global->LDS DMA
+    from L2) at 1 and 2 waves per SIMD."""
+    wgs = 256
+    ops = [rt.upload(bf16_rne(rng.standard_normal(wgs * 512 * 96, dtype=np.float32))), rt.alloc(wgs * 512 * 192)]
+    rec = rt.alloc(wgs * (32 + 4096))
+    out = {}
+    for name, src in (("mfma_issue_normal", ops[0]), ("mfma_issue_zeros", ops[1])):
+        f = lambda: rt.floor_mfma(src.gpu_addr(), rec.gpu_addr(), wgs, 2048)
+        ms = Timer(rt).run(f, steps, warmup)
+        f()
+        rt.wait_idle()
+        mhz, span, cyc = _clock_records(rec, wgs)
+        out[name] = {"us_per_launch": round(ms * 1e3, 2), "sclk_mhz": round(mhz, 1), "workgroup_us": round(span, 2),
+                     "workgroup_cycles": round(cyc), "mfma_cycles_per_simd": 4096 * 32}
+    src64 = rt.alloc(65536)
+    rates = {}
+    for mode, name, lane_bytes in ((0, "ds_read_b128", 128), (1, "ds_read_b64_tr_b16", 64), (2, "dma_to_lds", 128)):
+        for threads in (256, 512):
+            rounds = 2000
+            rt.floor_lds(mode, src64.gpu_addr(), rec.gpu_addr(), wgs, threads, rounds)
+            rt.wait_idle()
+            mhz, span, cyc = _clock_records(rec, wgs)
+            rates[f"{name}_{threads // 256}_wave_per_simd"] = round(threads * lane_bytes * rounds / cyc, 1)
+    out["lds_bytes_per_clk_per_cu"] = rates
+    for b in ops + [rec, src64]:
         b.free()
     return out
 

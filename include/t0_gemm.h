@@ -419,6 +419,22 @@ int t0_copy_device(t0_runtime* rt, uint64_t src, uint64_t dst, uint64_t bytes);
 int t0_floor_stream_read(t0_runtime* rt, uint64_t src, uint64_t bytes, uint64_t sink, uint32_t workgroups,
                          uint32_t threads);
 int t0_floor_empty(t0_runtime* rt, uint32_t workgroups, uint32_t threads);
+/* Ceilings of the compute-bound GEMM (measurement aids, no reference
+ * counterpart).  t0_floor_mfma issues mfma_per_wave (a multiple of 16)
+ * v_mfma_f32_32x32x16_bf16 per wave from registers on `workgroups` 512-thread
+ * workgroups, the 8-wave 256x256 tile's accumulators and operand
+ * fragments, nothing else in the loop; the fragments come from `operands`
+ * (workgroups * 512 * 192 bytes, 16-byte aligned), whose values set the
+ * power the MFMAs draw.  t0_floor_lds has every wave read its LDS window in
+ * rounds of 8 ds_read_b128 (mode 0) or ds_read_b64_tr_b16 (mode 1), or issue
+ * 8 one-KiB global->LDS DMAs from the 64 KiB `src` (mode 2), `rounds` times.
+ * Both write 4 u64 per workgroup to `out` -- the 100 MHz clock and the
+ * shader clock at start and end -- and need out to hold workgroups * 32
+ * bytes, plus workgroups * 2048 (t0_floor_mfma) or 4096 (t0_floor_lds) bytes
+ * that are written only on an impossible result.  Asynchronous. */
+int t0_floor_mfma(t0_runtime* rt, uint64_t operands, uint64_t out, uint32_t workgroups, uint32_t mfma_per_wave);
+int t0_floor_lds(t0_runtime* rt, int mode, uint64_t src, uint64_t out, uint32_t workgroups, uint32_t threads,
+                 uint32_t rounds);
 /* t0_unpad_2d (src/t0/math.rs): out[m][n] = padded[m][n_pad]. */
 int t0_unpad_2d(t0_runtime* rt, uint64_t padded, uint64_t out, uint32_t m, uint32_t n, uint32_t n_pad);
 

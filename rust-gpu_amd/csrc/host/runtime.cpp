@@ -1513,6 +1513,45 @@ int t0_floor_empty(t0_runtime* rt, uint32_t workgroups, uint32_t threads) {
     return launch(rt, f, workgroups, 1, 1, threads, p);
 }
 
+int t0_floor_mfma(t0_runtime* rt, uint64_t operands, uint64_t out, uint32_t workgroups, uint32_t mfma_per_wave) {
+    if (!rt || !operands || !out || operands % 16 || out % 8) return fail(T0_ERR_INVALID, "null or misaligned buffer");
+    if (!workgroups || !mfma_per_wave || mfma_per_wave % 16)
+        return fail(T0_ERR_INVALID, "workgroups > 0 and mfma_per_wave a positive multiple of 16");
+    int r = set_dev(rt);
+    if (r) return r;
+    hipFunction_t f;
+    r = get_fn(rt, "t0k_mfma_issue", &f);
+    if (r) return r;
+    t0_aux_params p;
+    memset(&p, 0, sizeof p);
+    p.src = (const void*)operands;
+    p.dst = (void*)out;
+    p.m = mfma_per_wave / 8;
+    p.n = 0x7FBADBADu;   // a signalling-NaN pattern no f32 sum produces
+    return launch(rt, f, workgroups, 1, 1, 512, p);
+}
+
+int t0_floor_lds(t0_runtime* rt, int mode, uint64_t src, uint64_t out, uint32_t workgroups, uint32_t threads,
+                 uint32_t rounds) {
+    static const char* const syms[] = {"t0k_lds_read_b128", "t0k_lds_read_tr16", "t0k_lds_dma"};
+    if (!rt || !out || out % 8 || mode < 0 || mode > 2 || (mode == 2 && (!src || src % 16)))
+        return fail(T0_ERR_INVALID, "bad arguments (mode 2 needs a 16-byte aligned 64 KiB source)");
+    if (!workgroups || !threads || threads % 64 || threads > 1024 || !rounds)
+        return fail(T0_ERR_INVALID, "bad launch shape");
+    int r = set_dev(rt);
+    if (r) return r;
+    hipFunction_t f;
+    r = get_fn(rt, syms[mode], &f);
+    if (r) return r;
+    t0_aux_params p;
+    memset(&p, 0, sizeof p);
+    p.src = (const void*)src;
+    p.dst = (void*)out;
+    p.m = rounds;
+    p.n = 0xDEADBEEFu;   // never equal to the xor of the LDS contents
+    return launch(rt, f, workgroups, 1, 1, threads, p);
+}
+
 int t0_unpad_2d(t0_runtime* rt, uint64_t padded, uint64_t out, uint32_t m, uint32_t n, uint32_t n_pad) {
     if (!rt || !padded || !out || n_pad < n) return fail(T0_ERR_INVALID, "bad arguments");
     int r = set_dev(rt);

@@ -339,3 +339,128 @@ extern "C" __global__ void __launch_bounds__(1024) t0k_stream_read(const t0_aux_
     if ((x[0] ^ x[1] ^ x[2] ^ x[3]) == p.m) ((uint32_t*)p.dst)[blockIdx.x] = 1u;
 }
 extern "C" __global__ void __launch_bounds__(1024) t0k_empty(const t0_aux_params p) {}
+
+// MFMA-issue floor of the 8-wave 256 x 256 GEMM: 512 threads per workgroup,
+// every wave loads two sets of operand fragments (4 A + 2 B, 16 bytes per
+// lane each, from src at (workgroup * 512 + thread) * 192 bytes) and issues
+// m rounds of the tile's 8 v_mfma_f32_32x32x16_bf16 on acc[4][2] from
+// registers, alternating the sets, with nothing else in the loop.  The
+// operand values set the power draw (and so the clock the part sustains);
+// the GEMM's own data gives its MFMA-only time.  dst receives 4 u64 per
+// workgroup: the 100 MHz clock and the shader clock at start and end
+// (thread 0, after a barrier at the end).  The sums are written (to dst
+// past the records) only if they equal n, a value the host never passes.
+extern "C" __global__ void __launch_bounds__(512) t0k_mfma_issue(const t0_aux_params p) {
+    const uint32_t tid = threadIdx.x, bid = blockIdx.x;
+    uint64_t* rec = (uint64_t*)p.dst + 4 * bid;
+    const uint64_t rt0 = __builtin_amdgcn_s_memrealtime(), st0 = __builtin_amdgcn_s_memtime();
+    const u32x4_t* d = (const u32x4_t*)p.src + ((size_t)bid * 512 + tid) * 12;
+    bf16x8_t af[2][4], bf[2][2];
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) af[s][i] = __builtin_bit_cast(bf16x8_t, d[s * 6 + i]);
+#pragma unroll
+        for (int j = 0; j < 2; j++) bf[s][j] = __builtin_bit_cast(bf16x8_t, d[s * 6 + 4 + j]);
+    }
+    f32x16_t acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = f32x16_t{};
+    for (uint32_t it = 0; it < p.m; it += 2) {
+#pragma unroll
+        for (int s = 0; s < 2; s++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[s][j], af[s][i], acc[i][j], 0, 0, 0);
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) sum += acc[i][j][r];
+    if (__float_as_uint(sum) == p.n) ((float*)((uint64_t*)p.dst + 4 * gridDim.x))[bid * 512 + tid] = sum;
+    __syncthreads();
+    if (tid == 0) {
+        rec[0] = rt0;
+        rec[1] = __builtin_amdgcn_s_memrealtime();
+        rec[2] = st0;
+        rec[3] = __builtin_amdgcn_s_memtime();
+    }
+}
+
+// LDS port rates per CU.  Every wave issues m rounds of 8 reads of its own
+// 8 KB window of a 64 KB LDS buffer (flags 0: ds_read_b128, 1:
+// ds_read_b64_tr_b16 at the GEMM's NN operand pattern), waiting for each
+// round; or (flags 2) 8 global -> LDS DMAs (buffer_load_dwordx4 ... lds,
+// 1 KB each) of a 64 KB source src that stays in L2.  dst receives the
+// workgroup records of t0k_mfma_issue.
+template <int MODE>
+__device__ __forceinline__ void lds_rate(const t0_aux_params& p) {
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[65536];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (uint32_t i = tid * 16; i < 65536; i += blockDim.x * 16) *(u32x4_t*)(smem + i) = u32x4_t{i, i + 1, i + 2, i + 3};
+    __syncthreads();
+    const uint64_t rt0 = __builtin_amdgcn_s_memrealtime(), st0 = __builtin_amdgcn_s_memtime();
+    const uint32_t base = (uint32_t)(uintptr_t)(LDS_AS uint8_t*)smem;
+    uint32_t acc = 0;
+    if constexpr (MODE == 0) {
+        const uint32_t a = base + ((wave * 8192 + lane * 16) & 65535);
+        for (uint32_t it = 0; it < p.m; it++) {
+            u32x4_t r0, r1, r2, r3, r4, r5, r6, r7;
+            asm volatile("ds_read_b128 %0, %8 offset:0\n\tds_read_b128 %1, %8 offset:1024\n\t"
+                         "ds_read_b128 %2, %8 offset:2048\n\tds_read_b128 %3, %8 offset:3072\n\t"
+                         "ds_read_b128 %4, %8 offset:4096\n\tds_read_b128 %5, %8 offset:5120\n\t"
+                         "ds_read_b128 %6, %8 offset:6144\n\tds_read_b128 %7, %8 offset:7168\n\t"
+                         "s_waitcnt lgkmcnt(0)"
+                         : "=v"(r0), "=v"(r1), "=v"(r2), "=v"(r3), "=v"(r4), "=v"(r5), "=v"(r6), "=v"(r7)
+                         : "v"(a));
+            acc ^= r0[0] ^ r1[1] ^ r2[2] ^ r3[3] ^ r4[0] ^ r5[1] ^ r6[2] ^ r7[3];
+        }
+    } else if constexpr (MODE == 1) {
+        // 16-lane groups read 4 rows x 32 B of a 512-byte-row tile (the NN
+        // B operand's access), rows swizzled as the GEMM stores them
+        const uint32_t g = lane >> 4, i16 = lane & 15;
+        const uint32_t a = base + ((wave * 8192 + (g >> 1) * 8 * 512 + (i16 >> 2) * 512 +
+                                    ((((g & 1) * 2 + (i16 & 3) / 2) ^ ((0xEA40u >> ((i16 >> 2) * 4)) & 0xFu)) * 16) +
+                                    (i16 & 1) * 8) & 65535);
+        for (uint32_t it = 0; it < p.m; it++) {
+            u32x2_t r0, r1, r2, r3, r4, r5, r6, r7;
+            asm volatile("ds_read_b64_tr_b16 %0, %8 offset:0\n\tds_read_b64_tr_b16 %1, %8 offset:64\n\t"
+                         "ds_read_b64_tr_b16 %2, %8 offset:128\n\tds_read_b64_tr_b16 %3, %8 offset:192\n\t"
+                         "ds_read_b64_tr_b16 %4, %8 offset:256\n\tds_read_b64_tr_b16 %5, %8 offset:320\n\t"
+                         "ds_read_b64_tr_b16 %6, %8 offset:384\n\tds_read_b64_tr_b16 %7, %8 offset:448\n\t"
+                         "s_waitcnt lgkmcnt(0)"
+                         : "=v"(r0), "=v"(r1), "=v"(r2), "=v"(r3), "=v"(r4), "=v"(r5), "=v"(r6), "=v"(r7)
+                         : "v"(a));
+            acc ^= r0[0] ^ r1[1] ^ r2[0] ^ r3[1] ^ r4[0] ^ r5[1] ^ r6[0] ^ r7[1];
+        }
+    } else {
+        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.src), (short)0, 65536,
+                                                                           0x00020000);
+        for (uint32_t it = 0; it < p.m; it++) {
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                t0::dma_x4(r, __builtin_amdgcn_readfirstlane(base + (((wave * 8 + j) * 1024) & 65535)),
+                           (lane * 16 + j * 1024) & 65535);
+            t0::wait_vmcnt_fence<0>();
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        uint64_t* rec = (uint64_t*)p.dst + 4 * blockIdx.x;
+        rec[0] = rt0;
+        rec[1] = __builtin_amdgcn_s_memrealtime();
+        rec[2] = st0;
+        rec[3] = __builtin_amdgcn_s_memtime();
+    }
+    if ((acc ^ smem[tid]) == p.n) ((uint32_t*)p.dst)[8 * gridDim.x + tid] = acc;
+}
+extern "C" __global__ void __launch_bounds__(1024) t0k_lds_read_b128(const t0_aux_params p) { lds_rate<0>(p); }
+extern "C" __global__ void __launch_bounds__(1024) t0k_lds_read_tr16(const t0_aux_params p) { lds_rate<1>(p); }
+extern "C" __global__ void __launch_bounds__(1024) t0k_lds_dma(const t0_aux_params p) { lds_rate<2>(p); }

@@ -461,6 +461,12 @@ class GpuRuntime:
     def floor_empty(self, workgroups=256, threads=1024):
         _check(lib().t0_floor_empty(self.h, workgroups, threads))
 
+    def floor_mfma(self, operands, out, workgroups=256, mfma_per_wave=2048):
+        _check(lib().t0_floor_mfma(self.h, operands, out, workgroups, mfma_per_wave))
+
+    def floor_lds(self, mode, src, out, workgroups=256, threads=512, rounds=2000):
+        _check(lib().t0_floor_lds(self.h, mode, src, out, workgroups, threads, rounds))
+
     def copy_device(self, src, dst, nbytes):
         _check(lib().t0_copy_device(self.h, src, dst, nbytes))
 

@@ -148,6 +148,8 @@ SIGNATURES = {
     "t0_copy_device": ([vp, u64, u64, u64], C.c_int),
     "t0_floor_stream_read": ([vp, u64, u64, u64, u32, u32], C.c_int),
     "t0_floor_empty": ([vp, u32, u32], C.c_int),
+    "t0_floor_mfma": ([vp, u64, u64, u32, u32], C.c_int),
+    "t0_floor_lds": ([vp, C.c_int, u64, u64, u32, u32, u32], C.c_int),
     "t0_bf16_matmul": ([vp, u64, u64, u64, u32, u32, u32], C.c_int),
     "t0_bf16_matmul_backward_data": ([vp, u64, u64, u64, u32, u32, u32], C.c_int),
     "t0_bf16_matmul_backward_weight": ([vp, u64, u64, u64, u32, u32, u32], C.c_int),

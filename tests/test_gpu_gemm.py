@@ -116,12 +116,15 @@ def _golden(golden_dir, name, dtype, shape):
     return np.fromfile(os.path.join(golden_dir, name), dtype=dtype).reshape(shape)
 
 
-def test_torch_fixture_gemm(rt, dev, golden_dir):
-    """benchmarks/torch_ref (seed 42): X[64,256] . W_gate[512,256]^T."""
+@pytest.mark.parametrize("w_name,ref_name,ref16_name", [("w_gate.bin", "h_gate_f32ref.bin", "h_gate_bf16acc.bin"),
+                                                        ("w_up.bin", "h_up_f32ref.bin", "h_up_bf16acc.bin")])
+def test_torch_fixture_gemm(rt, dev, golden_dir, w_name, ref_name, ref16_name):
+    """benchmarks/torch_ref (seed 42): X[64,256] . W_gate[512,256]^T and
+    X . W_up^T, f32 output and torch's bf16 output."""
     x = _golden(golden_dir, "x.bin", np.uint16, (64, 256))
-    w = _golden(golden_dir, "w_gate.bin", np.uint16, (512, 256))
-    ref32 = _golden(golden_dir, "h_gate_f32ref.bin", np.float32, (64, 512))
-    ref16 = _golden(golden_dir, "h_gate_bf16acc.bin", np.float32, (64, 512))
+    w = _golden(golden_dir, w_name, np.uint16, (512, 256))
+    ref32 = _golden(golden_dir, ref_name, np.float32, (64, 512))
+    ref16 = _golden(golden_dir, ref16_name, np.float32, (64, 512))
     tol = tolerance(f32(x), f32(w), 256)
     for cfg in (None, t0.GemmConfig.tile_64x64_k64(), t0.GemmConfig.tile_256x256_k64()):
         got = run_gemm(rt, dev, x, w, 64, 512, 256, t0.NT, t0.OUT_F32, cfg=cfg)
@@ -142,6 +145,11 @@ def test_torch_fixture_second_gemm(rt, dev, golden_dir):
     # same product in NN form
     got_nn = run_gemm(rt, dev, s, wd.T.copy(), 64, 256, 512, t0.NN, t0.OUT_F32)
     check_close(got_nn, ref, tolerance(f32(s), f32(wd), 512), "y nn")
+    # bf16 output against torch's bf16 chain (benchmarks/gen_torch_ref.py:141)
+    ref16 = _golden(golden_dir, "y_bf16chain.bin", np.float32, (64, 256))
+    g16 = run_gemm(rt, dev, s, wd, 64, 256, 512, t0.NT, t0.OUT_BF16)
+    assert np.mean(g16 == ref16) > 0.99
+    assert np.all(np.abs(g16 - ref16) <= np.abs(ref16) * 2.0**-7 + 1e-30)
 
 
 # ------------------------------------------------- instances beyond presets --

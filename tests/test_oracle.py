@@ -148,6 +148,40 @@ def test_gemm_nt_torch_fixture_bf16_output(golden_dir):
     assert np.all(np.abs(ours - ref) <= ulp + 1e-30)
 
 
+@pytest.mark.parametrize("w_name,ref_name,ref16_name", [("w_gate.bin", "h_gate_f32ref.bin", "h_gate_bf16acc.bin"),
+                                                        ("w_up.bin", "h_up_f32ref.bin", "h_up_bf16acc.bin")])
+def test_gemm_nt_torch_fixture_first_stage(golden_dir, w_name, ref_name, ref16_name):
+    """benchmarks/gen_torch_ref.py:102-117: both first-stage projections,
+    h_gate and h_up = X.float() @ W.float().T (f32) and torch.mm(X, W.T)
+    (bf16 output), M=64, K=256, N=512.  The oracle is within f32 rounding of
+    the exact sum, and its bf16 RNE agrees with torch's bf16 output up to
+    one ulp on near-ties."""
+    x = _load(golden_dir, "x.bin", np.uint16).reshape(64, 256)
+    w = _load(golden_dir, w_name, np.uint16).reshape(512, 256)
+    ref = _load(golden_dir, ref_name, np.float32).reshape(64, 512)
+    ref16 = _load(golden_dir, ref16_name, np.float32).reshape(64, 512)
+    y = orc.gemm_nt(x, w)
+    exact = orc.gemm_f64(x, w, "nt")
+    bound = 256 * 2.0**-24 * np.abs(orc.bf16_to_f32(x)).astype(np.float64) @ np.abs(orc.bf16_to_f32(w)).T
+    assert np.all(np.abs(y - exact) <= bound + 1e-30)
+    assert np.all(np.abs(ref - exact) <= bound + 1e-30)
+    ours16 = orc.bf16_to_f32(orc.bf16_rne(y))
+    assert np.mean(ours16 == ref16) > 0.999
+    assert np.all(np.abs(ours16 - ref16) <= np.abs(ref16) * 2.0**-7 + 1e-30)
+
+
+def test_gemm_nt_torch_fixture_second_gemm_bf16_chain(golden_dir):
+    """benchmarks/gen_torch_ref.py:141: y_bf16chain = torch.mm(swiglu_bf16_trunc,
+    W_down.T) with bf16 output (M=64, K=512, N=256): the oracle's f32 result
+    rounded to bf16 agrees up to one ulp on near-ties."""
+    s = _load(golden_dir, "swiglu_bf16_trunc.bin", np.uint16).reshape(64, 512)
+    wd = _load(golden_dir, "w_down.bin", np.uint16).reshape(256, 512)
+    ref16 = _load(golden_dir, "y_bf16chain.bin", np.float32).reshape(64, 256)
+    ours16 = orc.bf16_to_f32(orc.bf16_rne(orc.gemm_nt(s, wd)))
+    assert np.mean(ours16 == ref16) > 0.999
+    assert np.all(np.abs(ours16 - ref16) <= np.abs(ref16) * 2.0**-7 + 1e-30)
+
+
 def test_gemm_nt_torch_fixture_second_gemm(golden_dir):
     """y_bf16_f32acc = swiglu_bf16_trunc.float() @ W_down.float().T (M=64,K=512,N=256)."""
     s = _load(golden_dir, "swiglu_bf16_trunc.bin", np.uint16).reshape(64, 512)
