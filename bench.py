@@ -188,6 +188,60 @@ def bench_ceilings(rt, steps, warmup, rng):
     return out
 
 
+TILE_SHAPES = [(m, n, k) for m in (32, 128, 512, 1024, 2048, 4096)
+               for (n, k) in ((4096, 4096), (11008, 4096), (4096, 11008), (14336, 4096))] + \
+              [(4096, 1024, 4096), (3072, 8192, 4096), (384, 4096, 4096), (16, 4096, 4096)]
+
+
+def bench_tiles(rt, steps, warmup, rng, tr):
+    """Evidence for the tile / split-K selection (t0_auto_schedule_gemm,
+    src/t0/cost_model.rs:464-535): on LLM shapes (NN, N(0,1) bf16 operands,
+    bf16 out), every ranked candidate is timed with the weight operand B
+    rotated through copies that exceed the 256 MB Infinity Cache (read cold
+    from HBM, as in inference), as graph replays.  Per shape: the pick
+    (rank 0) and the measured best, their predicted and measured times, the
+    regret pick / best and the best's rank in the predicted order."""
+    rows = []
+    for (m, n, k) in TILE_SHAPES:
+        cands = t0.auto_schedule_gemm(m, n, k, t0.NN, t0.OUT_BF16)
+        rot = max(2, -(-300_000_000 // (k * n * 2)))
+        a = rt.upload(bf16_rne(rng.standard_normal((m, k), dtype=np.float32)))
+        bsets = [rt.upload(bf16_rne(rng.standard_normal((k, n), dtype=np.float32))) for _ in range(rot)]
+        c = rt.alloc(m * n * 2)
+        meas = []
+        for cfg, est in cands:
+            def one(i, cfg=cfg):
+                rt.gemm(a.gpu_addr(), bsets[i % rot].gpu_addr(), c.gpu_addr(), m, n, k, transpose=t0.NN,
+                        out_dtype=t0.OUT_BF16, cfg=cfg)
+            one(0)
+            rt.wait_idle()
+            g = rt.capture(lambda: [one(i) for i in range(rot)])
+            tm = Timer(rt)
+            ms = tm.run(g.launch, 5, 2, warm_ms=5.0) / rot
+            g.destroy()
+            meas.append(ms * 1e3)
+        for buf in bsets + [a, c]:
+            buf.free()
+        best = int(np.argmin(meas))
+        order = sorted(range(len(cands)), key=lambda i: cands[i][1])
+        rows.append({"shape": [m, n, k], "candidates": len(cands),
+                     "pick": f"{cands[0][0].name()} w{cands[0][0].wg_size // 64}",
+                     "pick_pred_us": round(cands[0][1], 2), "pick_us": round(meas[0], 2),
+                     "best": f"{cands[best][0].name()} w{cands[best][0].wg_size // 64}",
+                     "best_pred_us": round(cands[best][1], 2), "best_us": round(meas[best], 2),
+                     "regret": round(meas[0] / meas[best], 3), "best_rank_predicted": order.index(best),
+                     "median_abs_pred_err": round(float(np.median([abs(cands[i][1] / meas[i] - 1)
+                                                                   for i in range(len(cands))])), 3),
+                     "all": [[f"{cfg.name()} w{cfg.wg_size // 64}", round(est, 2), round(t, 2)]
+                             for (cfg, est), t in zip(cands, meas)]})
+        print(f"# tiles {m}x{n}x{k}: pick {rows[-1]['pick']} {meas[0]:.1f} us, best {rows[-1]['best']} "
+              f"{meas[best]:.1f} us (regret {rows[-1]['regret']})", file=sys.stderr, flush=True)
+    reg = [r["regret"] for r in rows]
+    return {"workload": "tile / split-K selection, NN bf16 out, B cold", "shapes": rows,
+            "regret_median": round(float(np.median(reg)), 3), "regret_max": round(float(np.max(reg)), 3),
+            "picks_within_3pct": sum(r <= 1.03 for r in reg), "shape_count": len(rows)}
+
+
 def load_traffic():
     p = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(p):
@@ -506,7 +560,7 @@ def main():
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="issue rotated launches directly (for tracers)")
     ap.add_argument("--only", choices=["gemm4096", "skinny", "decode", "prefill", "ignis", "norm_decode", "copy",
-                                       "floor"],
+                                       "floor", "tiles"],
                     default=None,
                     help="run one workload (for counter collection)")
     args = ap.parse_args()
@@ -525,7 +579,7 @@ def main():
     if args.only:
         fn = {"gemm4096": bench_gemm_4096, "skinny": bench_skinny, "decode": bench_decode,
               "prefill": bench_prefill, "ignis": bench_ignis, "norm_decode": bench_norm_decode,
-              "copy": bench_copy, "floor": bench_floor}[args.only]
+              "copy": bench_copy, "floor": bench_floor, "tiles": bench_tiles}[args.only]
         r = fn(rt, args.steps, args.warmup, rng, tr)
         for key in ("a", "b", "_host"):
             r.pop(key, None)

@@ -147,6 +147,14 @@ int t0_auto_select(uint32_t m, uint32_t k, uint32_t n, t0_gemm_config* out);
 /* Replaces auto_select_legacy (src/t0/gemm_gen.rs:351-404): the reference's
  * decision tree over the shapes, mapped onto gfx950 tiles. */
 int t0_auto_select_legacy(uint32_t m, uint32_t k, uint32_t n, t0_gemm_config* out);
+/* Replaces auto_schedule_gemm (src/t0/cost_model.rs:464-535): every
+ * feasible candidate for an m x n x k GEMM of this layout and output type,
+ * best first, with its predicted time in microseconds (the score).  Writes
+ * at most `cap` configs to out (and times to est_us, if not NULL); returns
+ * the number of candidates, or a negative status.  Its first entry is what
+ * t0_gemm selects when no tuning cache entry exists. */
+int t0_auto_schedule_gemm(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype,
+                          t0_gemm_config* out, double* est_us, uint32_t cap);
 /* Replaces prefill_spec_cache::cached_auto_select (src/t0/prefill_spec_cache.rs:55-76). */
 int t0_cached_auto_select(uint32_t m, uint32_t k, uint32_t n, t0_gemm_config* out);
 /* Replaces prefill_spec_cache::prewarm_cache (src/t0/prefill_spec_cache.rs:125-129). */

@@ -444,6 +444,18 @@ int t0_auto_select(uint32_t m, uint32_t k, uint32_t n, t0_gemm_config* out) {
     return T0_OK;
 }
 
+int t0_auto_schedule_gemm(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype,
+                          t0_gemm_config* out, double* est_us, uint32_t cap) {
+    if (!m || !n || !k || transpose > T0_NN || out_dtype > T0_OUT_BF16) return fail(T0_ERR_INVALID, "bad arguments");
+    if (cap && !out) return fail(T0_ERR_INVALID, "null output");
+    const auto c = rank_candidates(m, n, k, transpose, out_dtype, true);
+    for (uint32_t i = 0; i < cap && i < c.size(); i++) {
+        out[i] = c[i].cfg;
+        if (est_us) est_us[i] = c[i].est_us;
+    }
+    return (int)c.size();
+}
+
 int t0_auto_select_legacy(uint32_t m, uint32_t k, uint32_t n, t0_gemm_config* out) {
     // decision tree of auto_select_legacy (src/t0/gemm_gen.rs:351-404)
     if (!out) return fail(T0_ERR_INVALID, "null output");

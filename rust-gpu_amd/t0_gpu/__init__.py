@@ -130,6 +130,21 @@ def auto_select(m: int, k: int, n: int) -> GemmConfig:
     return _sel(lib().t0_auto_select, m, k, n)
 
 
+def auto_schedule_gemm(m: int, n: int, k: int, transpose=NT, out_dtype=OUT_F32) -> list:
+    """src/t0/cost_model.rs:464-535: every feasible candidate, best first, as
+    (GemmConfig, predicted microseconds)."""
+    count = _check(lib().t0_auto_schedule_gemm(m, n, k, transpose, out_dtype, None, None, 0))
+    raw = (GemmConfigC * count)()
+    est = (C.c_double * count)()
+    _check(lib().t0_auto_schedule_gemm(m, n, k, transpose, out_dtype, raw, est, count))
+    out = []
+    for i in range(count):
+        c = GemmConfig()
+        C.memmove(C.addressof(c), C.addressof(raw[i]), C.sizeof(GemmConfigC))
+        out.append((c, float(est[i])))
+    return out
+
+
 def auto_select_legacy(m: int, k: int, n: int) -> GemmConfig:
     return _sel(lib().t0_auto_select_legacy, m, k, n)
 
@@ -481,10 +496,15 @@ class Graph:
     def launch(self):
         _check(lib().t0_graph_launch(self.rt.h, self.h))
 
+    def destroy(self):
+        """Releases the graph (and its pin on the runtime's shared buffers)."""
+        if self.h:
+            lib().t0_graph_destroy(self.h)
+            self.h = None
+
     def __del__(self):
         try:
-            if self.h:
-                lib().t0_graph_destroy(self.h)
+            self.destroy()
         except Exception:
             pass
 

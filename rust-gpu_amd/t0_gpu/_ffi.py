@@ -82,6 +82,7 @@ SIGNATURES = {
     "t0_build_kernargs_backward_data": ([u64, u64, u64, u32, u32, u32, P(GemmConfigC), vp], C.c_int),
     "t0_build_kernargs_backward_weight": ([u64, u64, u64, u32, u32, u32, P(GemmConfigC), vp], C.c_int),
     "t0_auto_select": ([u32, u32, u32, P(GemmConfigC)], C.c_int),
+    "t0_auto_schedule_gemm": ([u32, u32, u32, u32, u32, P(GemmConfigC), P(C.c_double), u32], C.c_int),
     "t0_auto_select_legacy": ([u32, u32, u32, P(GemmConfigC)], C.c_int),
     "t0_cached_auto_select": ([u32, u32, u32, P(GemmConfigC)], C.c_int),
     "t0_prewarm_cache": ([P(u32), sz], C.c_int),

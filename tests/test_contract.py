@@ -198,6 +198,21 @@ def test_auto_select_takes_measured_best_on_llm_shapes():
     assert c.tile_m <= 128 and c.split_k == 4
 
 
+def test_auto_schedule_gemm_ranked_list():
+    """src/t0/cost_model.rs:464-535: the ranked candidate list is sorted by
+    predicted time, every entry is a feasible kernel of the requested layout
+    and output type, its head is what auto_select picks (NT, f32), and the
+    bf16-output list may split K (reduced in-kernel)."""
+    for (m, n, k) in ((4096, 4096, 4096), (128, 4096, 4096), (16, 11008, 4096), (1000, 3000, 200)):
+        lst = t0.auto_schedule_gemm(m, n, k, t0.NT, t0.OUT_F32)
+        assert lst and all(a[1] <= b[1] for a, b in zip(lst, lst[1:]))
+        assert all(c.transpose == t0.NT and c.out_dtype == t0.OUT_F32 for c, _ in lst)
+        assert lst[0][0].name() == t0.auto_select(m, k, n).name()
+        assert all(c.is_feasible() for c, _ in lst)
+    sk = [c for c, _ in t0.auto_schedule_gemm(128, 4096, 4096, t0.NN, t0.OUT_BF16) if c.split_k > 1]
+    assert sk and all(c.transpose == t0.NN and c.out_dtype == t0.OUT_BF16 for c in sk)
+
+
 def test_auto_select_legacy_preserved():
     """src/t0/gemm_gen.rs:606-617."""
     c = t0.auto_select_legacy(256, 256, 256)
