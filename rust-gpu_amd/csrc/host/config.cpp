@@ -153,32 +153,36 @@ static uint32_t est_vgprs(const GemmInstance& g) {
     return fm * fn * 16 + (fm + fn) * 8 + 48;
 }
 
-// Per-tile cost, calibrated on MI355X with every tile below at split 1..8
-// on 17 LLM shapes (NN, bf16 out, M = 32..4096, N = 1024..14336,
-// K = 1024..11008), B rotated through more copies than the 256 MB MALL holds
-// (a weight operand read cold from HBM, as in inference).  Predicted time:
+// Per-tile cost, fitted (t0_gpu/fit_tile_cost.py) to every ranked tile x
+// split-K candidate timed on MI355X by `bench.py --only tiles`: 28 LLM
+// shapes (NN, bf16 out, M = 16..4096, N = 1024..14336, K = 4096 or 11008),
+// the weight operand B rotated through more copies than the 256 MB MALL
+// holds (read cold from HBM, as in inference).  Predicted time:
 //   per workgroup  a + b * k_len / 1000 us while a round of workgroups
-//                  (CUs x workgroups per CU) is resident; a partly filled
-//                  last round costs DISC + (1 - DISC) * fill of a round;
+//                  (CUs x workgroups per CU, by LDS) is resident; a partly
+//                  filled last round costs DISC + (1 - DISC) * fill of a round;
 //   co-resident workgroups (2+ per CU) run at most 1/CO_RESIDENT as fast,
 //                  so ceil(workgroups / CUs) of them queue on one CU;
 //   memory         no faster than A + B + C over HBM_TBS, nor the operand
 //                  re-reads (A once per column tile, B once per row tile)
 //                  over L2_TBS;
-//   split-K        + FIX us + FIX_MB us per MB of partial planes.
-// Least squares on log time: median error 7 %; the pick is the measured best
-// on 10 of the 17 shapes and within 17 % on all.
+//   split-K        + FIX us + FIX_MB us per MB of partial tiles.
+// Least squares on log time: median error 9 %; the pick is within 3 % of
+// the measured best on 16 of the 28 shapes (also with each shape left out
+// of the fit), at most 27.5 % slower (32 x 11008 x 4096), and the measured
+// best is among the 4 best-predicted candidates on every shape, so the
+// tuner's candidates (t0_tune, top 8) always include it.
 struct TileCost {
     uint32_t bm, bn, bk, nw;
     double a_us, b_us;
 };
 constexpr TileCost kTileCost[] = {
-    {256, 256, 64, 8, 16.86, 19.07}, {256, 128, 64, 4, 10.01, 14.05}, {128, 256, 64, 4, 10.37, 14.44},
-    {128, 128, 64, 4, 4.79, 8.88}, {128, 64, 64, 4, 3.58, 6.47}, {64, 128, 64, 4, 3.19, 6.59},
-    {64, 64, 64, 1, 2.18, 9.54}, {32, 128, 64, 2, 4.66, 10.35}, {32, 64, 64, 1, 2.13, 6.80},
+    {256, 256, 64, 8, 21.31, 17.22}, {256, 128, 64, 4, 11.93, 12.65}, {128, 256, 64, 4, 12.84, 13.10},
+    {128, 128, 64, 4, 7.84, 7.50},   {128, 64, 64, 4, 5.16, 5.32},    {64, 128, 64, 4, 4.91, 5.52},
+    {64, 64, 64, 1, 4.37, 6.47},     {32, 128, 64, 2, 8.45, 6.25},    {32, 64, 64, 1, 3.19, 5.43},
 };
-constexpr double kDisc = 0.977, kFixUs = 2.282, kFixUsPerMB = 0.439;
-constexpr double kHbmTBs = 3.429, kL2TBs = 13.841, kCoResident = 0.618;
+constexpr double kDisc = 0.964, kFixUs = 1.430, kFixUsPerMB = 0.462;
+constexpr double kHbmTBs = 3.678, kL2TBs = 14.734, kCoResident = 0.517;
 
 std::vector<Candidate> rank_candidates(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype,
                                        bool allow_fixup) {

@@ -1,0 +1,159 @@
+"""Fits the per-tile cost table of rank_candidates (csrc/host/config.cpp,
+kTileCost and the constants beside it) to the measurements that
+``python bench.py --only tiles`` prints: every ranked tile x split-K
+candidate timed on LLM shapes (NN, bf16 out, weight operand read cold).
+
+    python rust-gpu_amd/t0_gpu/fit_tile_cost.py tiles.json
+
+The model is the one rank_candidates evaluates: per workgroup a + b * k_len
+/ 1000 us while a round of workgroups (CUs x workgroups per CU, by LDS) is
+resident, a partly filled last round costing DISC + (1 - DISC) * fill of a
+round; co-resident workgroups at most 1 / CO as fast each; no faster than
+A + B + C over HBM, nor the operand re-reads over L2; split-K adding FIX +
+FIX_MB per MB of partial tiles.  Least squares on log time from several
+starts; prints the fitted constants, the pick's regret (pick / measured
+best) per shape, and the same with each shape left out of the fit."""
+import json
+import math
+import re
+import sys
+
+import numpy as np
+from scipy.optimize import least_squares
+
+CUS, LDS = 256.0, 160 * 1024.0
+NAME = re.compile(r"t0_gemm_(\d+)x(\d+)_k(\d+)_ldsdb(?:_sk(\d+))?_nn_bf16 w(\d+)")
+# LDS bytes of each instance (stages x stage bytes, or the epilogue staging)
+STAGES = {(256, 256, 64, 8): 2, (256, 128, 64, 4): 3, (128, 256, 64, 4): 3, (128, 128, 64, 4): 4,
+          (128, 64, 64, 4): 4, (64, 128, 64, 4): 4, (64, 64, 64, 1): 4, (32, 128, 64, 2): 4, (32, 64, 64, 1): 6}
+WAVES = {(256, 256, 64, 8): (2, 4), (256, 128, 64, 4): (2, 2), (128, 256, 64, 4): (2, 2),
+         (128, 128, 64, 4): (2, 2), (128, 64, 64, 4): (2, 2), (64, 128, 64, 4): (2, 2), (64, 64, 64, 1): (1, 1),
+         (32, 128, 64, 2): (1, 2), (32, 64, 64, 1): (1, 1)}
+TILES = list(STAGES)
+
+
+def lds_bytes(t):
+    bm, bn, bk, nw = t
+    wm, wn = WAVES[t]
+    return max((bm + bn) * bk * 2 * STAGES[t], nw * 32 * (bn // wn + 4) * 4)
+
+
+def predict(params, t, sk, m, n, k):
+    ti = TILES.index(t)
+    a, b = params[2 * ti], params[2 * ti + 1]
+    disc, fix, fix_mb, hbm, l2, co = params[2 * len(TILES):]
+    bm, bn = t[0], t[1]
+    slots = CUS * max(1.0, min(math.floor(LDS / lds_bytes(t)), 8.0))
+    tiles = math.ceil(m / bm) * math.ceil(n / bn)
+    wgs = tiles * sk
+    full = math.floor(wgs / slots)
+    fill = wgs / slots - full
+    rounds = full + (disc + (1 - disc) * fill if fill > 0 else 0.0)
+    t_wg = a + b * (k / sk) / 1000.0
+    tm = rounds * t_wg
+    if slots > CUS:
+        tm = max(tm, math.ceil(wgs / CUS) * t_wg * co)
+    hb = k * n * 2.0 + m * k * 2.0 + m * n * 2.0
+    l2b = m * k * 2.0 * math.ceil(n / bn) + n * k * 2.0 * math.ceil(m / bm)
+    tm = max(tm, hb / (hbm * 1e6), l2b / (l2 * 1e6))
+    if sk > 1:
+        tm += fix + fix_mb * wgs * bm * bn * 4 / 1e6
+    return tm
+
+
+def load(path):
+    d = json.load(open(path))
+    data = []
+    for r in d["shapes"]:
+        m, n, k = r["shape"]
+        cands = []
+        for name, _est, meas in r["all"]:
+            g = NAME.fullmatch(name)
+            bm, bn, bk, sk, w = int(g[1]), int(g[2]), int(g[3]), int(g[4] or 1), int(g[5])
+            cands.append(((bm, bn, bk, w), sk, meas))
+        data.append(((m, n, k), cands))
+    return data
+
+
+def _arrays(data):
+    """Per-candidate arrays of the model's inputs (tile index, workgroups,
+    rounds structure, bytes) so that a prediction is a few numpy operations."""
+    rows = []
+    for (m, n, k), cands in data:
+        for t, sk, meas in cands:
+            bm, bn = t[0], t[1]
+            slots = CUS * max(1.0, min(math.floor(LDS / lds_bytes(t)), 8.0))
+            wgs = math.ceil(m / bm) * math.ceil(n / bn) * sk
+            hb = k * n * 2.0 + m * k * 2.0 + m * n * 2.0
+            l2b = m * k * 2.0 * math.ceil(n / bn) + n * k * 2.0 * math.ceil(m / bm)
+            rows.append((TILES.index(t), wgs / slots, slots > CUS, math.ceil(wgs / CUS), k / sk / 1000.0, hb, l2b,
+                         sk > 1, wgs * bm * bn * 4 / 1e6, meas))
+    a = np.array(rows, dtype=np.float64)
+    return {"ti": a[:, 0].astype(int), "q": a[:, 1], "co": a[:, 2] > 0, "qc": a[:, 3], "kl": a[:, 4],
+            "hb": a[:, 5], "l2": a[:, 6], "sk": a[:, 7] > 0, "mb": a[:, 8], "meas": a[:, 9]}
+
+
+def predict_all(p, A):
+    nt = len(TILES)
+    a, b = p[0:2 * nt:2][A["ti"]], p[1:2 * nt:2][A["ti"]]
+    disc, fix, fix_mb, hbm, l2, co = p[2 * nt:]
+    full = np.floor(A["q"])
+    fill = A["q"] - full
+    rounds = full + np.where(fill > 0, disc + (1 - disc) * fill, 0.0)
+    t_wg = a + b * A["kl"]
+    tm = rounds * t_wg
+    tm = np.where(A["co"], np.maximum(tm, A["qc"] * t_wg * co), tm)
+    tm = np.maximum(tm, np.maximum(A["hb"] / (hbm * 1e6), A["l2"] / (l2 * 1e6)))
+    return tm + np.where(A["sk"], fix + fix_mb * A["mb"], 0.0)
+
+
+def fit(data, starts=8, seed=0):
+    rng = np.random.default_rng(seed)
+    A = _arrays(data)
+
+    def resid(p):
+        return np.log(np.maximum(predict_all(p, A), 1e-3) / A["meas"])
+
+    lo = [0.1, 0.1] * len(TILES) + [0.5, 0.0, 0.0, 1.0, 2.0, 0.2]
+    hi = [60.0, 60.0] * len(TILES) + [1.0, 20.0, 5.0, 8.0, 40.0, 1.0]
+    best = None
+    for _ in range(starts):
+        x0 = [rng.uniform(l, h) for l, h in zip(lo, hi)]
+        r = least_squares(resid, x0, bounds=(lo, hi))
+        if best is None or r.cost < best.cost:
+            best = r
+    return best.x, float(np.median(np.abs(np.exp(best.fun) - 1)))
+
+
+def regrets(params, data):
+    out = []
+    for (m, n, k), cands in data:
+        pick = min(range(len(cands)), key=lambda i: predict(params, cands[i][0], cands[i][1], m, n, k))
+        best = min(c[2] for c in cands)
+        out.append(cands[pick][2] / best)
+    return out
+
+
+def main():
+    data = load(sys.argv[1])
+    params, med_err = fit(data)
+    reg = regrets(params, data)
+    print(f"fit: median |pred/meas - 1| {med_err:.3f}; pick regret median {np.median(reg):.3f}, "
+          f"max {max(reg):.3f}, within 3% on {sum(r <= 1.03 for r in reg)} of {len(reg)}")
+    for t, i in zip(TILES, range(len(TILES))):
+        print(f"    {{{t[0]}, {t[1]}, {t[2]}, {t[3]}, {params[2 * i]:.2f}, {params[2 * i + 1]:.2f}}},")
+    disc, fix, fix_mb, hbm, l2, co = params[2 * len(TILES):]
+    print(f"constexpr double kDisc = {disc:.3f}, kFixUs = {fix:.3f}, kFixUsPerMB = {fix_mb:.3f};")
+    print(f"constexpr double kHbmTBs = {hbm:.3f}, kL2TBs = {l2:.3f}, kCoResident = {co:.3f};")
+    loo = []
+    for j in range(len(data)):
+        p, _ = fit(data[:j] + data[j + 1:], starts=3, seed=j + 1)
+        loo.append(regrets(p, [data[j]])[0])
+    print(f"leave-one-shape-out regret: median {np.median(loo):.3f}, max {max(loo):.3f}, "
+          f"within 3% on {sum(r <= 1.03 for r in loo)} of {len(loo)}")
+    for (shape, _), r, rl in zip(data, reg, loo):
+        print(f"    {shape}: regret {r:.3f} (left out: {rl:.3f})")
+
+
+if __name__ == "__main__":
+    main()
