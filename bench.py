@@ -36,6 +36,7 @@ METRIC = "bf16 GEMM TFLOPS @4096³ (% MFMA peak); W4A16 decode HBM GB/s (% peak)
 PEAK_TFLOPS = 2516.6    # 256 CU x 2.4 GHz x 4096 dense bf16 FLOP/clk/CU
 PEAK_GBS = 8000.0       # HBM3E
 ROTATE = 12
+PARITY_ROWS = 64        # output rows of the 4096-row workloads checked against the oracle
 
 
 def bf16_rne(x: np.ndarray) -> np.ndarray:
@@ -285,6 +286,9 @@ def bench_gemm_4096(rt, steps, warmup, rng, tr):
     span = float(np.median([p[1] for p in probes]))
     flops = 2.0 * m * n * k
     tflops = flops / (ms * 1e-3) / 1e12
+    step()
+    rt.wait_idle()
+    gpu_rows = dc.read(np.uint16, PARITY_ROWS * n).reshape(PARITY_ROWS, n)
     for buf in (da, db, dc):
         buf.free()
     rf = roofline("mfma", tflops, PEAK_TFLOPS, "TFLOP/s", traffic_of(tr, "gemm_4096_nn_bf16"))
@@ -292,7 +296,7 @@ def bench_gemm_4096(rt, steps, warmup, rng, tr):
     rf["peak_at_measured_sclk"] = round(PEAK_TFLOPS * sclk / 2400.0, 1)
     rf["frac_at_measured_sclk"] = round(tflops / (PEAK_TFLOPS * sclk / 2400.0), 4)
     return {"ms": ms, "ms_median_per_launch": float(np.median(per)), "tflops": tflops, "kernel": cfg.name(),
-            "a": a, "b": b, "sclk_mhz": sclk, "workgroup_span_us": span, "roofline": rf}
+            "a": a, "b": b, "gpu_rows": gpu_rows, "sclk_mhz": sclk, "workgroup_span_us": span, "roofline": rf}
 
 
 def bench_skinny(rt, steps, warmup, rng, tr):
@@ -314,11 +318,14 @@ def bench_skinny(rt, steps, warmup, rng, tr):
     bytes_alg = m * k * 2 + k * n * 2 + m * n * 2
     gbs = bytes_alg / (ms * 1e-3) / 1e9
     tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+    one(0)
+    rt.wait_idle()
+    out0 = dc.read(np.uint16, m * n).reshape(m, n)
     for buf in bs + [da, dc]:
         buf.free()
     return {"workload": "skinny bf16 GEMM M=128 N=4096 K=4096 NN, bf16 out", "kernel": cfg.name(),
             "us_per_launch": round(ms * 1e3, 3), "us_median_per_launch": round(med * 1e3, 3),
-            "tflops": round(tflops, 2), "gbs": round(gbs, 1), "_host": (a, b0),
+            "tflops": round(tflops, 2), "gbs": round(gbs, 1), "_host": (a, b0, out0),
             "roofline": roofline("hbm", gbs, PEAK_GBS, "GB/s", traffic_of(tr, "gemm_skinny_128x4096x4096"))}
 
 
@@ -361,6 +368,9 @@ def bench_decode(rt, steps, warmup, rng, tr):
     # algorithmic bytes: W nibbles + bf16 scales + A + C (constant z not stored)
     bytes_alg = n * k // 2 + (k // gs) * n * 2 + m * k * 2 + m * n * 2
     gbs = bytes_alg / (ms * 1e-3) / 1e9
+    one(0)
+    rt.wait_idle()
+    out0 = dc.read(np.uint16, m * n).reshape(m, n)
     for s in sets:
         for buf in s:
             buf.free()
@@ -368,7 +378,7 @@ def bench_decode(rt, steps, warmup, rng, tr):
     dc.free()
     return {"workload": "W4A16 decode M=16 K=4096 N=11008, g=128, z=8, bf16 out", "kernel": plan[0],
             "split_k": plan[1], "us_per_launch": round(ms * 1e3, 3), "us_median_per_launch": round(med * 1e3, 3),
-            "gbs": round(gbs, 1), "bytes_per_launch": bytes_alg, "_host": (a_h, host0[0], host0[1]),
+            "gbs": round(gbs, 1), "bytes_per_launch": bytes_alg, "_host": (a_h, host0[0], host0[1], out0),
             "roofline": roofline("hbm", gbs, PEAK_GBS, "GB/s", traffic_of(tr, "w4a16_decode_16x4096x11008"))}
 
 
@@ -390,11 +400,12 @@ def bench_prefill(rt, steps, warmup, rng, tr):
     ms = tm.run(step, max(5, steps // 4), max(2, warmup // 2))
     med = float(np.median(tm.per_call(step, 20)))
     tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+    rows0 = dc.read(np.uint16, PARITY_ROWS * n).reshape(PARITY_ROWS, n)
     for buf in (a, dq, ds, dz, dc):
         buf.free()
     return {"workload": "W4A16 prefill M=4096 K=4096 N=14336, g=128, per-group z, bf16 out", "kernel": plan[0],
             "ms_per_launch": round(ms, 4), "ms_median_per_launch": round(med, 4), "tflops": round(tflops, 2),
-            "_host": (a_h, qw, s, zw),
+            "_host": (a_h, qw, s, zw, rows0),
             "roofline": roofline("mfma", tflops, PEAK_TFLOPS, "TFLOP/s", traffic_of(tr, "w4a16_prefill_4096x4096x14336"))}
 
 
@@ -482,52 +493,91 @@ def _cpu_entry(value, unit, sample, secs, extra=None):
 LOOP = "sequential-f32 no-FMA loop of examples/test_gemm_correctness.rs:28-42 (oracle restatement, one thread)"
 
 
-def cpu_baselines(head, extras, rows_big: int):
+def cpu_baselines(head, extras, rows_big: int, gpu_256=None):
     """The reference's CPU path on every BASELINE config (the same seeded
     inputs as the GPU run, in this process): C1 256^3 and C3 skinny in full;
     C4 decode in full as dequant (src/t0/quant_kernels.rs:365-372) then the
     same loop; C2 4096^3 and C5 prefill on a contiguous slice of rows_big M
-    rows, scaled by M / rows_big (the naive loop's cost is linear in M)."""
+    rows, scaled by M / rows_big (the naive loop's cost is linear in M).
+    Each config's GPU output is checked against the oracle result on the
+    same inputs (the first PARITY_ROWS rows of the 4096-row workloads):
+    max |err|, relative Frobenius error and the tight per-element bound of
+    oracle/parity.py."""
     from oracle import oracle as orc   # checker-side code: the CPU baseline leg only
+    from oracle import parity
     out = {}
+
+    def f32(u16):
+        return orc.bf16_to_f32(u16)
+
+    def check(got, ref, bound, rows):
+        """The GPU output against the oracle on the same inputs: max |err|,
+        relative Frobenius error, and the tight per-element bound."""
+        err = np.abs(np.asarray(got, np.float64) - np.asarray(ref, np.float64))
+        return {"outputs": int(err.size), "rows": rows, "max_abs_err": float(f"{err.max():.4g}"),
+                "rel_frobenius": float(f"{parity.rel_frobenius(got, ref):.4g}"),
+                "within_tight_bound": bool(np.all(err <= bound))}
+
+    def w4_parts(qw, sc, zw, zc, nn_, kk):
+        q = orc.int4_unpack(qw.view(np.uint8), nn_ * kk).reshape(nn_, kk)
+        G = kk // 128
+        if zw is None:
+            z = np.full((G, nn_), zc)
+        else:
+            z = np.zeros((G, nn_), np.int64)
+            for j in range(8):
+                z[:, j::8] = ((zw >> np.uint32(4 * j)) & 0xF).astype(np.int64)
+        return q, f32(sc), z
+
     # C2: 4096^3 NN, bf16 inputs N(0,1)
     a, b = head["a"], head["b"]
     m, k = a.shape
     n = b.shape[1]
     t = time.perf_counter()
-    orc.gemm_rows(a, b, "nn", 0, rows_big)
+    ref = orc.gemm_rows(a, b, "nn", 0, rows_big)
     dt = time.perf_counter() - t
+    pr = min(rows_big, PARITY_ROWS)
+    got = f32(head["gpu_rows"][:pr])
+    parity_head = check(got, ref[:pr], parity.tight_bound(ref[:pr], f32(a[:pr]), f32(b), True), f"0-{pr - 1}")
     out["gemm_4096"] = _cpu_entry(2.0 * rows_big * n * k / dt / 1e12, "TFLOP/s",
                                   f"rows 0-{rows_big - 1} of the 4096^3 NN GEMM ({2.0 * rows_big * n * k / 1e9:.2f} "
                                   f"GFLOP), {LOOP}; scaled to all {m} rows (cost linear in rows): "
                                   f"{dt * m / rows_big:.0f} s for the whole GEMM", dt)
+    out["parity_gemm_4096"] = parity_head
     # C1: 256^3, U(-1,1) inputs, f32 out, in full
     rng = np.random.default_rng(256)
     a1 = bf16_rne(rng.uniform(-1, 1, (256, 256)).astype(np.float32))
     b1 = bf16_rne(rng.uniform(-1, 1, (256, 256)).astype(np.float32))
     t = time.perf_counter()
-    orc.gemm_nn(a1, b1)
+    ref1 = orc.gemm_nn(a1, b1)
     dt = time.perf_counter() - t
     out["gemm_256"] = _cpu_entry(2.0 * 256 ** 3 / dt / 1e12, "TFLOP/s", f"whole 256^3 GEMM (U(-1,1) seed 256), {LOOP}",
                                  dt)
+    if gpu_256 is not None:
+        out["parity_gemm_256"] = check(gpu_256(a1, b1), ref1, parity.tight_bound(ref1, f32(a1), f32(b1), False),
+                                       "all (f32 out)")
     # C3: skinny 128x4096x4096, in full
     if "skinny" in extras:
-        a3, b3 = extras["skinny"]["_host"]
+        a3, b3, g3 = extras["skinny"]["_host"]
         t = time.perf_counter()
-        orc.gemm_nn(a3, b3)
+        ref3 = orc.gemm_nn(a3, b3)
         dt = time.perf_counter() - t
+        extras["skinny"]["parity"] = check(f32(g3), ref3, parity.tight_bound(ref3, f32(a3), f32(b3), True), "all")
         fl = 2.0 * 128 * 4096 * 4096
         by = 128 * 4096 * 2 + 4096 * 4096 * 2 + 128 * 4096 * 2
         out["skinny"] = _cpu_entry(fl / dt / 1e12, "TFLOP/s", f"whole 128x4096x4096 GEMM (weight set 0), {LOOP}", dt,
                                    {"gbs": round(by / dt / 1e9, 4)})
     # C4: decode, dequant + loop, in full
     if "w4a16_decode" in extras:
-        a4, qw, sc = extras["w4a16_decode"]["_host"]
+        a4, qw, sc, g4 = extras["w4a16_decode"]["_host"]
         mm, kk, nn_ = a4.shape[0], a4.shape[1], qw.shape[0]
         t = time.perf_counter()
         w = orc.w4a16_dequant(qw, sc, None, 8, nn_, kk, 128)
-        orc.gemm_bf16_f32w_rows(a4, w, 0, mm)
+        ref4 = orc.gemm_bf16_f32w_rows(a4, w, 0, mm)
         dt = time.perf_counter() - t
+        q, sf, z = w4_parts(qw, sc, None, 8, nn_, kk)
+        extras["w4a16_decode"]["parity"] = check(f32(g4), ref4,
+                                                 parity.w4_tight_bound(ref4, f32(a4), q, sf, z, 128, True), "all")
         by = extras["w4a16_decode"]["bytes_per_launch"]
         out["w4a16_decode"] = _cpu_entry(by / dt / 1e9, "GB/s",
                                          f"whole 16x4096x11008 decode (weight set 0): dequant (q - 8) * s to f32, then "
@@ -535,13 +585,17 @@ def cpu_baselines(head, extras, rows_big: int):
                                          {"tflops": round(2.0 * mm * nn_ * kk / dt / 1e12, 6)})
     # C5: prefill, dequant + a row slice of the loop
     if "w4a16_prefill" in extras:
-        a5, qw, sc, zw = extras["w4a16_prefill"]["_host"]
+        a5, qw, sc, zw, g5 = extras["w4a16_prefill"]["_host"]
         mm, kk, nn_ = a5.shape[0], a5.shape[1], qw.shape[0]
         t = time.perf_counter()
         w = orc.w4a16_dequant(qw, sc, zw, 0, nn_, kk, 128)
         t_dq = time.perf_counter() - t
-        orc.gemm_bf16_f32w_rows(a5, w, 0, rows_big)
+        ref5 = orc.gemm_bf16_f32w_rows(a5, w, 0, rows_big)
         t_loop = time.perf_counter() - t - t_dq
+        q, sf, z = w4_parts(qw, sc, zw, 0, nn_, kk)
+        extras["w4a16_prefill"]["parity"] = check(f32(g5[:pr]), ref5[:pr],
+                                                  parity.w4_tight_bound(ref5[:pr], f32(a5[:pr]), q, sf, z, 128, True),
+                                                  f"0-{pr - 1}")
         total = t_dq + t_loop * mm / rows_big
         out["w4a16_prefill"] = _cpu_entry(2.0 * mm * nn_ * kk / total / 1e12, "TFLOP/s",
                                           f"dequant of the whole 14336x4096 weight ({t_dq:.1f} s) + rows 0-{rows_big - 1}"
@@ -581,7 +635,7 @@ def main():
               "prefill": bench_prefill, "ignis": bench_ignis, "norm_decode": bench_norm_decode,
               "copy": bench_copy, "floor": bench_floor, "tiles": bench_tiles}[args.only]
         r = fn(rt, args.steps, args.warmup, rng, tr)
-        for key in ("a", "b", "_host"):
+        for key in ("a", "b", "gpu_rows", "_host"):
             r.pop(key, None)
         print(json.dumps({"only": args.only, **{k: v for k, v in r.items()}}, default=float), flush=True)
         rt.close()
@@ -599,11 +653,22 @@ def main():
             shown = {k: v for k, v in extras[name].items() if k != "_host"}
             print(f"# {name}: {json.dumps(shown)}", file=sys.stderr, flush=True)
     cpu = None
+    parity_head = None
     if not args.no_cpu_baseline:
-        cpus = cpu_baselines(head, extras, args.cpu_rows)
+        def gpu_256(a1, b1):
+            """The CPU config (256^3, U(-1,1), f32 out) on the GPU, for its parity entry."""
+            d1, e1, c1 = rt.upload(a1), rt.upload(b1), rt.alloc(256 * 256 * 4)
+            rt.gemm(d1.gpu_addr(), e1.gpu_addr(), c1.gpu_addr(), 256, 256, 256, transpose=t0.NN, out_dtype=t0.OUT_F32)
+            rt.wait_idle()
+            r1 = c1.read(np.float32, 256 * 256).reshape(256, 256)
+            for x in (d1, e1, c1):
+                x.free()
+            return r1
+        cpus = cpu_baselines(head, extras, args.cpu_rows, gpu_256)
         cpu = cpus.pop("gemm_4096")
+        parity_head = cpus.pop("parity_gemm_4096")
         extras["cpu_gemm_256"] = {"workload": "bf16 GEMM M=N=K=256, U(-1,1), f32 out (CPU-only config)",
-                                  "cpu_baseline": cpus.pop("gemm_256")}
+                                  "cpu_baseline": cpus.pop("gemm_256"), "parity": cpus.pop("parity_gemm_256", None)}
         for key, v in cpus.items():
             extras[key]["cpu_baseline"] = v
     for e in extras.values():
@@ -630,6 +695,7 @@ def main():
                    "workgroup_span_us": round(head["workgroup_span_us"], 2)},
         "roofline": head["roofline"],
         "cpu_baseline": cpu,
+        "parity": parity_head,
         "extras": extras,
     }
     print(json.dumps(line), flush=True)
