@@ -1410,11 +1410,11 @@ int t0_w4a16_gemm(t0_runtime* rt, const t0_w4a16_desc* d) {
         p.semaphores = rt->sem;
     }
     if (pl.kind == 2) {
-        // workspace: R[g][m] = group row sums of A; bf16 scales widened to
-        // f32 [G][N] (the prefill reads f32 scales); a 2 KiB tail the
-        // row-sum DMA may touch
+        // workspace: [G][M] x 16 B, the group row sums of A as the
+        // prefill's correction operand; bf16 scales widened to f32 [G][N]
+        // (the prefill reads f32 scales); a 2 KiB tail
         const uint32_t G = p.K / 128;
-        const size_t r_bytes = ((size_t)G * p.M * 4 + 255) & ~(size_t)255;
+        const size_t r_bytes = ((size_t)G * p.M * 16 + 255) & ~(size_t)255;
         const bool widen = !d->scales_f32;
         r = ensure_ws(rt, r_bytes + (widen ? (size_t)G * p.N * 4 : 0) + 2048);
         if (r) return r;

@@ -383,7 +383,8 @@ __device__ __forceinline__ void w4_decode(const t0_w4a16_params& p) {
 //     A  [BM][128] bf16, 16-B chunks swizzled by row         BM*256 B
 //     W  [BN][16 words] packed nibbles, chunk-swizzled         BN*64 B
 //     S  [BN] f32 scales of this group                         BN*4 B (1 KB slot)
-//     R  [BM] f32: sum_k a[m][k] over this group                BM*4 B
+//     R  [BM] x 16 B: the correction block's A operand of row m BM*16 B
+//        (R_m = sum_k a[m][k] over this group, split by w4_rowsum)
 //   MFMA step kk (0..7) takes, in lane half h, the 8 k of word h*8 + kk, so a
 //   lane reads its W column as two 16-B LDS loads per group.
 //   Per group T = sum_k a[m][k] * (q[k][n] - z_n), exactly as MFMA products:
@@ -394,7 +395,7 @@ __device__ __forceinline__ void w4_decode(const t0_w4a16_params& p) {
 //       times (an exact bf16 integer), the other 13 k zero;
 //   then acc += s_n * T, one FMA per output per group.
 // Requires: group_size == 128, K % 128 == 0, lda % 8 == 0, N % 8 == 0,
-//           R precomputed by w4_rowsum into workspace [G][M], f32 scales
+//           R precomputed by w4_rowsum into workspace [G][M] x 16 B, f32 scales
 //           (bf16 scales are widened by the same pre-pass).
 // ---------------------------------------------------------------------------
 template <int CH>
@@ -410,7 +411,9 @@ struct W4Cfg {
     // write zeros), the zero-point DMA 64 x 4 B: separate slots.
     static constexpr int S_BYTES = 2048;                 // scales [0, 1024), zero-point words [1024, 1280)
     static constexpr int Z_OFF = 1024;
-    static constexpr int X_BYTES = (BM * 4 + 1023) / 1024 * 1024;
+    static constexpr int X_BYTES = BM * 16;
+    static constexpr int X_LOADS = X_BYTES / 1024;    // 1-KB row-sum DMAs per stage
+    static constexpr int XW = NW - 2;                  // issued by waves 2.., at most two each
     static constexpr int STAGE = A_BYTES + W_BYTES + S_BYTES + X_BYTES;
     static constexpr int A_LOADS = A_BYTES / (1024 * NW);
     static constexpr int W_LOADS = W_BYTES / (1024 * NW);
@@ -418,11 +421,11 @@ struct W4Cfg {
     static constexpr int SMEM = (STAGE * STAGES > NW * 32 * EPI_LD * 4) ? STAGE * STAGES : NW * 32 * EPI_LD * 4;
     static_assert(A_LOADS >= 1 && A_LOADS * 1024 * NW == A_BYTES, "A split");
     static_assert(W_LOADS >= 1 && W_LOADS * 1024 * NW == W_BYTES, "W split");
-    static_assert(BN * 4 <= Z_OFF && BM * 4 <= 1024 * 2, "S/Z/X slots");
-    static_assert(NW >= 3, "S, Z and X DMAs go out from three different waves");
+    static_assert(BN * 4 <= Z_OFF && BM % 64 == 0, "S/Z/X slots");
+    static_assert(NW >= 3 && X_LOADS <= 2 * XW, "S, Z and X DMAs: waves 0, 1 and 2..");
     static_assert(SMEM <= 160 * 1024, "LDS");
     static_assert(STAGES == 2 || STAGES == 3, "stage waits below");
-    // loads every wave issues per stage; waves 0, 1 and NW-1 add the scale,
+    // loads every wave issues per stage; waves 0, 1 and 2.. add the scale,
     // zero-point and row-sum DMAs, so a wait for MIN_LOADS outstanding covers
     // one stage in flight on every wave (a wave with extras waits slightly longer)
     static constexpr int MIN_LOADS = A_LOADS + W_LOADS;
@@ -448,7 +451,7 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
     const uint8_t* A0 = (const uint8_t*)p.A + (size_t)m0 * lda * 2;
     const uint8_t* W0 = (const uint8_t*)p.qweight + (size_t)n0 * (K / 2);
     const uint8_t* S0 = (const uint8_t*)p.scales + (size_t)n0 * 4;   // f32
-    const float* X = p.workspace;   // [G][M]
+    const uint8_t* X = (const uint8_t*)p.workspace;   // [G][M] x 16 B
 
     // per-lane DMA offsets
     uint32_t a_off[G::A_LOADS], w_off[G::W_LOADS];
@@ -468,15 +471,21 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
     }
     const uint32_t s_off = (lane * 16 < BN * 4 && n0 + lane * 4 < N) ? lane * 16 : OOB_OFFSET;
     const uint32_t z_off = (lane < BN / 8 && n0 + lane * 8 < N) ? lane * 4 : OOB_OFFSET;   // zero-point word per lane
-    const uint32_t x_off = (lane * 16 < BM * 4 && m0 + lane * 4 < M) ? lane * 16 : OOB_OFFSET;
-    const uint32_t x_off2 = (1024 + lane * 16 < BM * 4 && m0 + 256 + lane * 4 < M) ? 1024 + lane * 16 : OOB_OFFSET;
+    // row-sum DMA x (one row per lane) goes out from wave 2 + x % XW as its
+    // extra load x / XW
+    uint32_t x_off[2];
+#pragma unroll
+    for (int xq = 0; xq < 2; xq++) {
+        const uint32_t x = wave - 2 + xq * G::XW, row = x * 64 + lane;
+        x_off[xq] = (wave >= 2 && x < (uint32_t)G::X_LOADS && m0 + row < M) ? row * 16 : OOB_OFFSET;
+    }
     const uint32_t lds_base = (uint32_t)(uintptr_t)(LDS_AS uint8_t*)smem;
 
     // The q-th load of this wave for stage t: its A chunks, its W chunks,
     // then (one wave each) the scales, the zero-point words and the row sums.
     constexpr int NQ = G::A_LOADS + G::W_LOADS + 2;
     auto issue_q = [&](uint32_t t, int q) {
-        const uint32_t st = lds_base + (t % STAGES) * G::STAGE;
+        const uint32_t st = lds_base + __builtin_amdgcn_readfirstlane((t % STAGES) * G::STAGE);
         if (q < G::A_LOADS) {
             dma_x4(make_rsrc(A0 + (size_t)t * 256), __builtin_amdgcn_readfirstlane(st + (wave_s * G::A_LOADS + q) * 1024),
                    a_off[q]);
@@ -497,12 +506,11 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
             if (q == 0 && p.zeros)
                 dma_x1(make_rsrc(p.zeros + (size_t)t * (N / 8) + n0 / 8),
                        __builtin_amdgcn_readfirstlane(st + G::A_BYTES + G::W_BYTES + G::Z_OFF), z_off);
-        } else if (wave_s == G::NW - 1) {
-            const __amdgpu_buffer_rsrc_t rx = make_rsrc(X + (size_t)t * M + m0);
-            if (q == 0)
-                dma_x4(rx, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + G::W_BYTES + G::S_BYTES), x_off);
-            else if (BM * 4 > 1024)
-                dma_x4(rx, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + G::W_BYTES + G::S_BYTES + 1024), x_off2);
+        } else {
+            const uint32_t x = wave_s - 2 + q * G::XW;
+            if (x < (uint32_t)G::X_LOADS)
+                dma_x4(make_rsrc(X + ((size_t)t * M + m0) * 16),
+                       __builtin_amdgcn_readfirstlane(st + G::A_BYTES + G::W_BYTES + G::S_BYTES + x * 1024), x_off[q]);
         }
     };
     auto issue = [&](uint32_t t) {
@@ -545,20 +553,15 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
     // scales at the start of the next step, under the first half's MFMAs.
     const bool late = G::NW >= 8 && ((wave >> 2) & 1);
 
-    // The correction block's operands from this lane's zero-point word and
-    // row sums: B column -(128 + z) in k 0..2 of lane half 0, A row R split
-    // hi/mid/lo (hi + mid + lo == R exactly) likewise.
-    auto zcol_of = [&](uint32_t zw, uint32_t col) {
-        const uint32_t z = p.zeros ? (zw >> (4 * (col % 8))) & 0xFu : p.zero_const;
+    // The correction block's B operand from this lane's zero-point word:
+    // column -(128 + z) in k 0..2 of lane half 0, zero elsewhere (the A
+    // operand, R split hi/mid/lo with hi + mid + lo == R exactly, comes
+    // ready-made from w4_rowsum).
+    const uint32_t z_sh = 4 * (l32 % 8);   // wn*TN + j*32 is a multiple of 8
+    auto zcol_of = [&](uint32_t zw) {
+        const uint32_t z = p.zeros ? (zw >> z_sh) & 0xFu : p.zero_const;
         const uint32_t zb = h ? 0u : 0xC300u + z;                     // bf16 -(128 + z)
         return __builtin_bit_cast(bf16x8_t, u32x4_t{zb | (zb << 16), zb, 0u, 0u});
-    };
-    auto rrow_of = [&](float r) {
-        const uint32_t hi = __float_as_uint(r) & 0xFFFF0000u;
-        const float r1 = r - __uint_as_float(hi);                       // exact
-        const uint32_t mid = __float_as_uint(r1) & 0xFFFF0000u;
-        const uint32_t lo = __float_as_uint(r1 - __uint_as_float(mid)); // <= 8 significant bits: exact in bf16
-        return __builtin_bit_cast(bf16x8_t, u32x4_t{(hi >> 16) | mid, lo >> 16, 0u, 0u});
     };
 
     if constexpr (STAGES == 3) {
@@ -571,6 +574,20 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
         // wait, and the two waves of a SIMD drift apart instead of starting
         // every step in the same phase.
         constexpr int PER = (NQ + 3) / 4;
+        // This lane's LDS byte offsets within a stage, fixed for the loop: a
+        // read adds the stage's offset (one SGPR) to one of these, the tile
+        // row/column block goes into the instruction's immediate offset.
+        uint32_t a_lo[8];
+#pragma unroll
+        for (int kk = 0; kk < 8; kk++) a_lo[kk] = a_row0 + ((h * 8 + kk) ^ a_sw) * 16;
+        const uint32_t col0 = wn * G::TN + l32;
+        const uint32_t w_lo0 = G::A_BYTES + col0 * 64 + w_c0, w_lo1 = G::A_BYTES + col0 * 64 + w_c1;
+        const uint32_t z_lo = G::A_BYTES + G::W_BYTES + G::Z_OFF + (col0 / 8) * 4;
+        const uint32_t s_lo = G::A_BYTES + G::W_BYTES + (wn * G::TN + 4 * h) * 4;
+        const uint32_t x_lo = G::A_BYTES + G::W_BYTES + G::S_BYTES + (wm * G::TM + l32) * 16;
+        auto stage_at = [&](uint32_t u) {
+            return (const LDS_AS uint8_t*)smem + __builtin_amdgcn_readfirstlane((u % STAGES) * G::STAGE);
+        };
         issue(0);
         if (nk > 1) issue(1);
         if (nk > 1) wait_vmcnt<G::MIN_LOADS>();
@@ -579,37 +596,31 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
         bf16x8_t af[2][G::FM];
         u32x4_t wlo[G::FN], whi[G::FN], wlo_n[G::FN], whi_n[G::FN];
         uint32_t zw[G::FN], zw_n[G::FN];
-        float xr[G::FM], xr_n[G::FM];
-        // step u's first operands, from stage u's buffer
-        auto read_first = [&](uint32_t u, bf16x8_t* a0, u32x4_t* wl, u32x4_t* wh, uint32_t* z, float* x) {
-            const LDS_AS uint8_t* st = (const LDS_AS uint8_t*)smem + (u % STAGES) * G::STAGE;
-            const LDS_AS uint32_t* sz = (const LDS_AS uint32_t*)(st + G::A_BYTES + G::W_BYTES + G::Z_OFF);
-            const LDS_AS float* sx = (const LDS_AS float*)(st + G::A_BYTES + G::W_BYTES + G::S_BYTES);
+        bf16x8_t xr[G::FM], xr_n[G::FM];
+        // a step's first operands, from its stage's buffer st
+        auto read_first = [&](const LDS_AS uint8_t* st, bf16x8_t* a0, u32x4_t* wl, u32x4_t* wh, uint32_t* z,
+                              bf16x8_t* x) {
 #pragma unroll
             for (int i = 0; i < G::FM; i++) {
-                a0[i] = *(const LDS_AS bf16x8_t*)(st + a_row0 + i * 32 * 256 + ((h * 8) ^ a_sw) * 16);
-                x[i] = h ? 0.0f : sx[wm * G::TM + i * 32 + l32];
+                a0[i] = *(const LDS_AS bf16x8_t*)(st + a_lo[0] + i * 32 * 256);
+                x[i] = *(const LDS_AS bf16x8_t*)(st + x_lo + i * 32 * 16);
             }
 #pragma unroll
             for (int j = 0; j < G::FN; j++) {
-                const uint32_t col = wn * G::TN + j * 32 + l32;
-                const LDS_AS uint8_t* wr = st + G::A_BYTES + col * 64;
-                wl[j] = *(const LDS_AS u32x4_t*)(wr + w_c0);
-                wh[j] = *(const LDS_AS u32x4_t*)(wr + w_c1);
-                z[j] = p.zeros ? sz[col / 8] : 0u;
+                wl[j] = *(const LDS_AS u32x4_t*)(st + w_lo0 + j * 32 * 64);
+                wh[j] = *(const LDS_AS u32x4_t*)(st + w_lo1 + j * 32 * 64);
+                z[j] = p.zeros ? *(const LDS_AS uint32_t*)(st + z_lo + j * 32 / 8 * 4) : 0u;
             }
         };
-        if (nk) read_first(0, af[0], wlo, whi, zw, xr);
+        if (nk) read_first(stage_at(0), af[0], wlo, whi, zw, xr);
         for (uint32_t t = 0; t < nk; t++) {
             if (late && t > 0) scale_add();
-            const LDS_AS uint8_t* sa = (const LDS_AS uint8_t*)smem + (t % STAGES) * G::STAGE;
-            const LDS_AS float* ss = (const LDS_AS float*)(sa + G::A_BYTES + G::W_BYTES);
+            const LDS_AS uint8_t* sa = stage_at(t);
 #pragma unroll
             for (int i = 0; i < G::FM; i++)
 #pragma unroll
                 for (int j = 0; j < G::FN; j++)
-                    tmp[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(zcol_of(zw[j], wn * G::TN + j * 32 + l32),
-                                                                        rrow_of(xr[i]), f32x16_t{}, 0, 0, 0);
+                    tmp[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(zcol_of(zw[j]), xr[i], f32x16_t{}, 0, 0, 0);
 #pragma unroll
             for (int kk = 0; kk < 8; kk++) {
                 const int cur = kk & 1;
@@ -629,12 +640,10 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
                 }
                 if (kk + 1 < 8) {
 #pragma unroll
-                    for (int i = 0; i < G::FM; i++) {
-                        const uint32_t c = (h * 8 + kk + 1) ^ a_sw;
-                        af[cur ^ 1][i] = *(const LDS_AS bf16x8_t*)(sa + a_row0 + i * 32 * 256 + c * 16);
-                    }
+                    for (int i = 0; i < G::FM; i++)
+                        af[cur ^ 1][i] = *(const LDS_AS bf16x8_t*)(sa + a_lo[kk + 1] + i * 32 * 256);
                 } else if (t + 1 < nk) {
-                    read_first(t + 1, af[cur ^ 1], wlo_n, whi_n, zw_n, xr_n);
+                    read_first(stage_at(t + 1), af[cur ^ 1], wlo_n, whi_n, zw_n, xr_n);
                 }
                 // the next sub-step's reads stay ahead of this one's MFMAs
                 // (the scheduler would sink them next to their uses, into
@@ -653,7 +662,7 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
             for (int j = 0; j < G::FN; j++) {
 #pragma unroll
                 for (int q4 = 0; q4 < 4; q4++)
-                    sv[j][q4] = *(const LDS_AS f32x4_t*)(ss + wn * G::TN + j * 32 + 8 * q4 + 4 * h);
+                    sv[j][q4] = *(const LDS_AS f32x4_t*)(sa + s_lo + (j * 32 + 8 * q4) * 4);
                 wlo[j] = wlo_n[j];
                 whi[j] = whi_n[j];
                 zw[j] = zw_n[j];
@@ -682,10 +691,9 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
         const LDS_AS uint8_t* sw = st + G::A_BYTES;
         const LDS_AS float* ss = (const LDS_AS float*)(st + G::A_BYTES + G::W_BYTES);
         const LDS_AS uint32_t* sz = (const LDS_AS uint32_t*)(st + G::A_BYTES + G::W_BYTES + G::Z_OFF);
-        const LDS_AS float* sx = (const LDS_AS float*)(st + G::A_BYTES + G::W_BYTES + G::S_BYTES);
+        const LDS_AS uint8_t* sx = st + G::A_BYTES + G::W_BYTES + G::S_BYTES;
 
-        // this lane's W words, and the correction block's operands: B column
-        // -(128 + z) in k 0..2 of lane half 0, A row R split hi/mid/lo likewise
+        // this lane's W words, and the correction block's operands
         bf16x8_t af[2][G::FM];
 #pragma unroll
         for (int i = 0; i < G::FM; i++)
@@ -698,19 +706,11 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
             const LDS_AS uint8_t* wr = sw + col * 64;
             wlo[j] = *(const LDS_AS u32x4_t*)(wr + w_c0);
             whi[j] = *(const LDS_AS u32x4_t*)(wr + w_c1);
-            const uint32_t z = p.zeros ? (sz[col / 8] >> (4 * (col % 8))) & 0xFu : p.zero_const;
-            const uint32_t zb = h ? 0u : 0xC300u + z;                     // bf16 -(128 + z)
-            zcol[j] = __builtin_bit_cast(bf16x8_t, u32x4_t{zb | (zb << 16), zb, 0u, 0u});
+            zcol[j] = zcol_of(p.zeros ? sz[col / 8] : 0u);
         }
 #pragma unroll
-        for (int i = 0; i < G::FM; i++) {
-            const float r = h ? 0.0f : sx[wm * G::TM + i * 32 + l32];
-            const uint32_t hi = __float_as_uint(r) & 0xFFFF0000u;
-            const float r1 = r - __uint_as_float(hi);                       // exact
-            const uint32_t mid = __float_as_uint(r1) & 0xFFFF0000u;
-            const uint32_t lo = __float_as_uint(r1 - __uint_as_float(mid)); // <= 8 significant bits: exact in bf16
-            rrow[i] = __builtin_bit_cast(bf16x8_t, u32x4_t{(hi >> 16) | mid, lo >> 16, 0u, 0u});
-        }
+        for (int i = 0; i < G::FM; i++)
+            rrow[i] = *(const LDS_AS bf16x8_t*)(sx + (wm * G::TM + i * 32 + l32) * 16);
 #pragma unroll
         for (int i = 0; i < G::FM; i++)
 #pragma unroll
@@ -769,7 +769,10 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
 }
 
 // Prefill pre-pass (group 128), 256 threads per block:
-//   R[g][m] = sum_{k in group g} a[m][k] into workspace [G][M];
+//   R = sum_{k in group g} a[m][k], written to workspace [G][M] x 16 B as
+//   the prefill's correction A operand: bf16 k0..k2 = hi, mid, lo with
+//   hi + mid + lo == R exactly (each piece holds the next 8 significant
+//   bits; f32 has 24), k3..k7 zero;
 //   with bf16 scales, the blocks past the row sums widen them to f32 into
 //   p.scales_f32 [G][N] (four per thread).
 __device__ __forceinline__ void w4_rowsum(const t0_w4a16_params& p) {
@@ -804,7 +807,13 @@ __device__ __forceinline__ void w4_rowsum(const t0_w4a16_params& p) {
     s += __shfl_xor(s, 1);
     s += __shfl_xor(s, 2);
     s += __shfl_xor(s, 4);
-    if (g < G && (lane % 8) == 0) p.workspace[(size_t)g * p.M + m] = s;
+    if (g < G && (lane % 8) == 0) {
+        const uint32_t hi = __float_as_uint(s) & 0xFFFF0000u;
+        const float r1 = s - __uint_as_float(hi);                       // exact
+        const uint32_t mid = __float_as_uint(r1) & 0xFFFF0000u;
+        const uint32_t lo = __float_as_uint(r1 - __uint_as_float(mid)); // <= 8 significant bits: exact in bf16
+        ((u32x4_t*)p.workspace)[(size_t)g * p.M + m] = u32x4_t{(hi >> 16) | mid, lo >> 16, 0u, 0u};
+    }
 }
 
 // Generic W4A16 (any M, N, group size dividing K): one thread per output,
