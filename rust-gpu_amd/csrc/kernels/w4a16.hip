@@ -612,15 +612,19 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
                 z[j] = p.zeros ? *(const LDS_AS uint32_t*)(st + z_lo + j * 32 / 8 * 4) : 0u;
             }
         };
-        if (nk) read_first(stage_at(0), af[0], wlo, whi, zw, xr);
+        // tmp[i][j] = the group's correction block, then its 8 sub-steps
+        auto correction = [&](int i) {
+#pragma unroll
+            for (int j = 0; j < G::FN; j++)
+                tmp[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(zcol_of(zw[j]), xr[i], f32x16_t{}, 0, 0, 0);
+        };
+        if (nk) {
+            read_first(stage_at(0), af[0], wlo, whi, zw, xr);
+#pragma unroll
+            for (int i = 0; i < G::FM; i++) correction(i);
+        }
         for (uint32_t t = 0; t < nk; t++) {
-            if (late && t > 0) scale_add();
             const LDS_AS uint8_t* sa = stage_at(t);
-#pragma unroll
-            for (int i = 0; i < G::FM; i++)
-#pragma unroll
-                for (int j = 0; j < G::FN; j++)
-                    tmp[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(zcol_of(zw[j]), xr[i], f32x16_t{}, 0, 0, 0);
 #pragma unroll
             for (int kk = 0; kk < 8; kk++) {
                 const int cur = kk & 1;
@@ -669,9 +673,23 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
             }
 #pragma unroll
             for (int i = 0; i < G::FM; i++) xr[i] = xr_n[i];
-            if (!late) scale_add();
+            // Per row block: this group's scale FMAs, then the next group's
+            // correction block into the same tmp.  Block i's FMAs run while
+            // the MFMAs of the blocks after it are still in flight, instead
+            // of all 64 waiting for the last MFMA and holding back the next
+            // group's first MFMA.
+#pragma unroll
+            for (int i = 0; i < G::FM; i++) {
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int j = 0; j < G::FN; j++)
+#pragma unroll
+                    for (int e = 0; e < 16; e++) acc[i][j][e] = fmaf(sv[j][e / 4][e % 4], tmp[i][j][e], acc[i][j][e]);
+                __builtin_amdgcn_sched_barrier(0);
+                correction(i);   // after the last group: unused, on the last group's operands
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
-        if (late && nk) scale_add();
     } else {
 #pragma unroll
     for (int s = 0; s < STAGES - 1; s++)
