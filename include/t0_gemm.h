@@ -363,6 +363,23 @@ int t0_tuner_invalidate(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, 
  * (NT, f32 out, like the reference). */
 int t0_auto_gemm(t0_runtime* rt, uint64_t a, uint64_t b, uint64_t c, uint32_t m, uint32_t n, uint32_t k,
                  double* tflops_out);
+/* One timed candidate of t0_tile_tune. */
+typedef struct t0_tile_tune_entry {
+    t0_tile_gemm spec;
+    double tflops;
+} t0_tile_tune_entry;
+/* Replaces cost_model::tune_tile_ir and TileIrTuneResult
+ * (src/t0/cost_model.rs:824-1080): for an NT tile_ir GEMM (bf16 in, f32
+ * out), the tile_ir_MxNxK.json cache in the tuner's directory if it holds a
+ * usable gfx950 tile; otherwise the reference's presets, then the cost
+ * model's tiles, each timed through the tile_ir dispatch path on seeded
+ * N(0,1) operands (median of the tuner's n_iters launches), the fastest
+ * cached.  Writes the best spec and its TFLOP/s, up to `cap` timed
+ * candidates fastest first to all (may be NULL), their count to *n_all
+ * (0 from the cache, whose file keeps only names) and whether the result
+ * came from the cache to *from_cache. */
+int t0_tile_tune(t0_runtime* rt, uint32_t m, uint32_t n, uint32_t k, t0_tile_gemm* best, double* best_tflops,
+                 t0_tile_tune_entry* all, uint32_t cap, uint32_t* n_all, int* from_cache);
 
 /* ------------------------------------------------------------------ INT4 */
 /* Replaces GptqWeight (src/t0/quant_kernels.rs:188-296): parse / measure the

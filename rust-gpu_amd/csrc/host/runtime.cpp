@@ -317,31 +317,41 @@ bool tuned_config_ok(const t0_gemm_config& c) {
            c.out_dtype <= T0_OUT_BF16;
 }
 
-bool load_cache_file(uint32_t m, uint32_t n, uint32_t k, uint32_t tr, uint32_t od, const char* arch,
-                     t0_gemm_config* cfg, double* tf) {
-    std::ifstream f(cache_file(m, n, k, tr, od));
+// Flat JSON objects as the tuners write them: the text of one field's value
+// (quotes dropped), or a number.
+bool read_text(const std::string& path, std::string* s) {
+    std::ifstream f(path);
     if (!f) return false;
     std::stringstream ss;
     ss << f.rdbuf();
-    const std::string s = ss.str();
-    auto raw = [&](const char* name, std::string* out) {
-        const std::string pat = std::string("\"") + name + "\":";
-        size_t p = s.find(pat);
-        if (p == std::string::npos) return false;
-        p += pat.size();
-        while (p < s.size() && (s[p] == ' ' || s[p] == '"')) p++;
-        size_t e = p;
-        while (e < s.size() && s[e] != '"' && s[e] != ',' && s[e] != '}') e++;
-        *out = s.substr(p, e - p);
-        return true;
-    };
-    auto num = [&](const char* name, double* v) {
-        std::string t;
-        if (!raw(name, &t) || t.empty()) return false;
-        char* end = nullptr;
-        *v = strtod(t.c_str(), &end);
-        return end && *end == 0;
-    };
+    *s = ss.str();
+    return true;
+}
+bool json_raw(const std::string& s, const char* name, std::string* out) {
+    const std::string pat = std::string("\"") + name + "\":";
+    size_t p = s.find(pat);
+    if (p == std::string::npos) return false;
+    p += pat.size();
+    while (p < s.size() && (s[p] == ' ' || s[p] == '"')) p++;
+    size_t e = p;
+    while (e < s.size() && s[e] != '"' && s[e] != ',' && s[e] != '}') e++;
+    *out = s.substr(p, e - p);
+    return true;
+}
+bool json_num(const std::string& s, const char* name, double* v) {
+    std::string t;
+    if (!json_raw(s, name, &t) || t.empty()) return false;
+    char* end = nullptr;
+    *v = strtod(t.c_str(), &end);
+    return end && *end == 0;
+}
+
+bool load_cache_file(uint32_t m, uint32_t n, uint32_t k, uint32_t tr, uint32_t od, const char* arch,
+                     t0_gemm_config* cfg, double* tf) {
+    std::string s;
+    if (!read_text(cache_file(m, n, k, tr, od), &s)) return false;
+    auto raw = [&](const char* name, std::string* out) { return json_raw(s, name, out); };
+    auto num = [&](const char* name, double* v) { return json_num(s, name, v); };
     std::string a;
     if (raw("arch", &a) && a != arch) return false;
     double tm, tn, tk, wg, t;
@@ -383,6 +393,66 @@ bool save_cache_file(uint32_t m, uint32_t n, uint32_t k, uint32_t tr, uint32_t o
       << ",\"swap\":" << (c.swap_grid ? "true" : "false") << ",\"tflops\":" << num << ",\"all\":[]"
       << ",\"arch\":\"" << arch << "\",\"transpose\":\"" << (tr == T0_NN ? "nn" : "nt") << "\",\"out_dtype\":\""
       << (od == T0_OUT_BF16 ? "bf16" : "f32") << "\",\"name\":\"" << config_name(c) << "\"}\n";
+    return (bool)f;
+}
+
+// tile_ir tuning results, tile_ir_MxNxK.json beside the GEMM tuner's files in
+// the reference's layout (src/t0/cost_model.rs:1083-1150: tile_m, tile_n,
+// tile_k, split_k, wgp, tflops, all); files written here add "arch" and
+// "waves".  A file for another architecture, or a tile no gfx950 kernel
+// runs, is ignored.
+std::string tile_cache_file(uint32_t m, uint32_t n, uint32_t k) {
+    return cache_dir() + "/tile_ir_" + std::to_string(m) + "x" + std::to_string(n) + "x" + std::to_string(k) + ".json";
+}
+
+t0_tile_gemm tile_spec(uint32_t bm, uint32_t bn, uint32_t bk, uint32_t waves, uint32_t split_k) {
+    t0_tile_gemm s;
+    memset(&s, 0, sizeof s);
+    s.tile_m = bm; s.tile_n = bn; s.tile_k = bk;
+    s.waves_per_wg = waves;
+    s.split_k = split_k;
+    s.double_buffer = 1; s.swap_grid = 1;   // the reference's defaults (src/t0/cost_model.rs:1107-1120)
+    s.transpose = T0_NT;
+    s.out_dtype = T0_OUT_F32;
+    return s;
+}
+
+bool load_tile_cache(uint32_t m, uint32_t n, uint32_t k, const char* arch, t0_tile_gemm* spec, double* tf) {
+    std::string s, a;
+    if (!read_text(tile_cache_file(m, n, k), &s)) return false;
+    if (json_raw(s, "arch", &a) && a != arch) return false;
+    double tm, tn, tk, t, sk = 1, w = 0;
+    if (!json_num(s, "tile_m", &tm) || !json_num(s, "tile_n", &tn) || !json_num(s, "tile_k", &tk) ||
+        !json_num(s, "tflops", &t))
+        return false;
+    json_num(s, "split_k", &sk);
+    json_num(s, "waves", &w);
+    t0_tile_gemm c = tile_spec((uint32_t)tm, (uint32_t)tn, (uint32_t)tk, (uint32_t)w, sk > 1 ? (uint32_t)sk : 1);
+    c.wgp_mode = s.find("\"wgp\":true") != std::string::npos;
+    const uint32_t q = c.split_k;
+    if (!tile_instance(c) || q > 16 || (q & (q - 1))) return false;
+    if (!w) c.waves_per_wg = tile_instance(c)->nw();
+    *spec = c;
+    *tf = t;
+    return true;
+}
+
+bool save_tile_cache(uint32_t m, uint32_t n, uint32_t k, const char* arch, const t0_tile_gemm& c, double tf,
+                     const std::vector<std::pair<t0_tile_gemm, double>>& all) {
+    const std::string d = cache_dir();
+    mkdir(d.c_str(), 0755);
+    std::ofstream f(tile_cache_file(m, n, k));
+    if (!f) return false;
+    char num[32];
+    snprintf(num, sizeof num, "%.2f", tf);
+    f << "{\"tile_m\":" << c.tile_m << ",\"tile_n\":" << c.tile_n << ",\"tile_k\":" << c.tile_k
+      << ",\"split_k\":" << (c.split_k > 1 ? c.split_k : 1) << ",\"wgp\":" << (c.wgp_mode ? "true" : "false")
+      << ",\"tflops\":" << num << ",\"all\":[";
+    for (size_t i = 0; i < all.size(); i++) {
+        snprintf(num, sizeof num, "%.2f", all[i].second);
+        f << (i ? "," : "") << "[\"" << tile_name(all[i].first) << "\"," << num << "]";
+    }
+    f << "],\"arch\":\"" << arch << "\",\"waves\":" << c.waves_per_wg << "}\n";
     return (bool)f;
 }
 
@@ -1217,6 +1287,123 @@ int t0_auto_gemm(t0_runtime* rt, uint64_t a, uint64_t b, uint64_t c, uint32_t m,
     r = t0_gemm(rt, &cfg, &d);
     if (r) return r;
     return t0_wait_idle(rt);
+}
+
+int t0_tile_tune(t0_runtime* rt, uint32_t m, uint32_t n, uint32_t k, t0_tile_gemm* best_out, double* tflops_out,
+                 t0_tile_tune_entry* all_out, uint32_t cap, uint32_t* n_all, int* from_cache) {
+    // src/t0/cost_model.rs:855-1080
+    if (!rt || !m || !n || !k || !best_out) return fail(T0_ERR_INVALID, "bad arguments");
+    if (n_all) *n_all = 0;
+    if (from_cache) *from_cache = 0;
+    t0_tile_gemm spec;
+    double tf = 0;
+    {
+        std::lock_guard<std::mutex> g(tuner().mu);
+        if (load_tile_cache(m, n, k, rt->arch.c_str(), &spec, &tf)) {   // 1. the cache file
+            *best_out = spec;
+            if (tflops_out) *tflops_out = tf;
+            if (from_cache) *from_cache = 1;
+            return T0_OK;
+        }
+    }
+    int r = set_dev(rt);
+    if (r) return r;
+    // 2a. the reference's proven presets (:877-896), with its filters, mapped
+    //     to the gfx950 kernel of each geometry
+    std::vector<t0_tile_gemm> cands;
+    std::set<std::string> seen;
+    auto add = [&](const t0_tile_gemm& c) {
+        const GemmInstance* g = tile_instance(c);
+        if (!g) return;
+        t0_tile_gemm x = c;
+        x.waves_per_wg = g->nw();
+        if (seen.insert(tile_name(x) + "#w" + std::to_string(g->nw())).second) cands.push_back(x);
+    };
+    static const uint32_t presets[][3] = {{128, 128, 64}, {128, 128, 32}, {128, 128, 16}, {128, 64, 32},
+                                          {128, 64, 16},  {64, 64, 16},   {32, 64, 16}};
+    for (const auto& q : presets) {
+        if (k % q[2]) continue;
+        if (q[0] > m && m >= 32) continue;
+        if (q[1] > n && n >= 32) continue;
+        add(tile_spec(q[0], q[1], q[2], 0, 1));
+    }
+    // 2b. the cost model's tiles (split 1, as tile_auto_select), best first
+    uint32_t from_model = 0;
+    for (const auto& c : rank_candidates(m, n, k, T0_NT, T0_OUT_F32, false)) {
+        if (split_of(c.cfg) != 1 || from_model >= tuner().max_candidates) continue;
+        const GemmInstance* g = instance_for(c.cfg);
+        add(tile_spec(g->bm, g->bn, g->bk, g->nw(), 1));
+        from_model++;
+    }
+    if (cands.empty()) return fail(T0_ERR_INFEASIBLE, "tile_tune: no candidates for %ux%ux%u", m, n, k);
+    // 3. seeded N(0,1) bf16 operands (the reference zero-fills them,
+    //    :1004-1009; constant data runs the MFMAs at a higher clock)
+    void *da, *db, *dc;
+    HIPCHK(hipMalloc(&da, (size_t)m * k * 2));
+    HIPCHK(hipMalloc(&db, (size_t)n * k * 2));
+    HIPCHK(hipMalloc(&dc, (size_t)m * n * 4));
+    {
+        std::vector<uint16_t> h(std::max((size_t)m * k, (size_t)n * k));
+        fill_normal_bf16(h.data(), (size_t)m * k, 0x9E3779B97F4A7C15ull);
+        HIPCHK(hipMemcpy(da, h.data(), (size_t)m * k * 2, hipMemcpyHostToDevice));
+        fill_normal_bf16(h.data(), (size_t)n * k, 0xD1B54A32D192ED03ull);
+        HIPCHK(hipMemcpy(db, h.data(), (size_t)n * k * 2, hipMemcpyHostToDevice));
+    }
+    // 4. each candidate through the tile_ir dispatch path: warm-up, then the
+    //    median of per-launch event timings
+    hipEvent_t e0, e1;
+    hipEventCreate(&e0);
+    hipEventCreate(&e1);
+    std::vector<std::pair<t0_tile_gemm, double>> res;
+    for (const auto& c : cands) {
+        t0_kernel* kern = nullptr;
+        uint8_t ka[96];
+        size_t len = 0;
+        uint32_t grid[3];
+        if (t0_ensure_tile_kernel(rt, &c, &kern) ||
+            t0_tile_build_kernargs_m((uint64_t)da, (uint64_t)db, (uint64_t)dc, k, n, m, &c, 0, 0, 1.0f, 0.0f, 0.0f,
+                                     ka, &len) ||
+            t0_tile_compute_grid(&c, m, n, grid))
+            continue;
+        bool ok = true;
+        for (int w = 0; w < 3 && ok; w++) ok = t0_dispatch_async(rt, kern, grid, ka, len) >= 0;
+        std::vector<float> times;
+        for (uint32_t it = 0; ok && it < tuner().n_iters; it++) {
+            hipEventRecord(e0, rt->stream);
+            if (t0_dispatch_async(rt, kern, grid, ka, len) < 0) { ok = false; break; }
+            hipEventRecord(e1, rt->stream);
+            hipEventSynchronize(e1);
+            float ms = 0;
+            hipEventElapsedTime(&ms, e0, e1);
+            times.push_back(ms);
+        }
+        if (!ok || times.empty()) {
+            if (rt->poisoned.load()) break;   // :1037-1041
+            continue;
+        }
+        std::sort(times.begin(), times.end());
+        const double us = times[times.size() / 2] * 1e3;
+        res.push_back({c, 2.0 * m * n * k / (us * 1e-6) / 1e12});
+    }
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    hipStreamSynchronize(rt->stream);
+    hipFree(da); hipFree(db); hipFree(dc);
+    if (res.empty()) return fail(T0_ERR_HIP, "tile_tune: every candidate failed");
+    // 5. fastest first; the best is cached
+    std::stable_sort(res.begin(), res.end(), [](const auto& a, const auto& b) { return a.second > b.second; });
+    {
+        std::lock_guard<std::mutex> g(tuner().mu);
+        save_tile_cache(m, n, k, rt->arch.c_str(), res[0].first, res[0].second, res);
+    }
+    *best_out = res[0].first;
+    if (tflops_out) *tflops_out = res[0].second;
+    for (size_t i = 0; all_out && i < res.size() && i < cap; i++) {
+        all_out[i].spec = res[i].first;
+        all_out[i].tflops = res[i].second;
+    }
+    if (n_all) *n_all = (uint32_t)res.size();
+    return T0_OK;
 }
 
 // ------------------------------------------------------------------- INT4 --

@@ -20,7 +20,8 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import _ffi
-from ._ffi import GemmConfigC, GemmDescC, GemmGeometryC, GptqViewC, KernelLoadConfigC, TileGemmC, W4A16DescC, lib
+from ._ffi import (GemmConfigC, GemmDescC, GemmGeometryC, GptqViewC, KernelLoadConfigC, TileGemmC, TileTuneEntryC,
+                   W4A16DescC, lib)
 
 NT, NN = 0, 1
 EPI_STORE_F32, EPI_BIAS_ADD, EPI_BIAS_ADD_RELU = 0, 1, 2
@@ -583,6 +584,33 @@ class GemmTuner:
     def invalidate(m: int, n: int, k: int, transpose=NT, out_dtype=OUT_F32):
         """GemmTuner::invalidate (src/t0/auto_gemm.rs:503-507)."""
         _check(lib().t0_tuner_invalidate(m, n, k, transpose, out_dtype))
+
+
+@dataclass
+class TileIrTuneResult:
+    """src/t0/cost_model.rs:824-833: the best tile_ir spec, its TFLOP/s, every
+    timed candidate as (name, tflops) fastest first (empty from the cache)."""
+    best: TileGemm
+    best_tflops: float
+    all: list
+    from_cache: bool
+
+
+def tune_tile_ir(rt: GpuRuntime, m: int, n: int, k: int) -> TileIrTuneResult:
+    """cost_model::tune_tile_ir (src/t0/cost_model.rs:855-1080); the cache
+    directory and the number of timed launches are GemmTuner's."""
+    best, tf = TileGemm(), C.c_double()
+    cap = 64
+    entries = (TileTuneEntryC * cap)()
+    n_all, cached = C.c_uint32(), C.c_int()
+    _check(lib().t0_tile_tune(rt.h, m, n, k, C.byref(best), C.byref(tf), entries, cap, C.byref(n_all),
+                              C.byref(cached)))
+    timed = []
+    for e in entries[:min(n_all.value, cap)]:
+        s = TileGemm()
+        C.memmove(C.byref(s), C.byref(e.spec), C.sizeof(TileGemmC))
+        timed.append((s.name(), e.tflops))
+    return TileIrTuneResult(best, tf.value, timed, bool(cached.value))
 
 
 def auto_gemm(rt: GpuRuntime, a: int, b: int, c: int, m: int, n: int, k: int) -> float:

@@ -36,6 +36,10 @@ class TileGemmC(C.Structure):
                 ("n_epilogue", u8), ("epilogue", u8 * 8), ("reserved", u8 * 3)]
 
 
+class TileTuneEntryC(C.Structure):
+    _fields_ = [("spec", TileGemmC), ("tflops", C.c_double)]
+
+
 class KernelLoadConfigC(C.Structure):
     _fields_ = [("workgroup_size", u32 * 3), ("lds_size", u32), ("kernarg_size", u32)]
 
@@ -136,6 +140,7 @@ SIGNATURES = {
     "t0_tune": ([vp, u32, u32, u32, u32, u32, P(GemmConfigC), P(f64)], C.c_int),
     "t0_tuner_set_cache_dir": ([cp], C.c_int),
     "t0_tuner_set_params": ([u32, u32], C.c_int),
+    "t0_tile_tune": ([vp, u32, u32, u32, P(TileGemmC), P(f64), P(TileTuneEntryC), u32, P(u32), P(C.c_int)], C.c_int),
     "t0_auto_gemm": ([vp, u64, u64, u64, u32, u32, u32, P(f64)], C.c_int),
     "t0_gptq_from_bytes": ([vp, sz, P(GptqViewC)], C.c_int),
     "t0_gptq_gpu_buffer_size": ([P(GptqViewC)], sz),

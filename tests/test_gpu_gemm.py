@@ -481,6 +481,42 @@ def test_tuner_and_auto_gemm(rt, dev, tmp_path):
                 "auto_gemm")
 
 
+def test_tune_tile_ir(rt, dev, tmp_path):
+    """src/t0/cost_model.rs:855-1150: tune_tile_ir times the reference's
+    presets and the cost model's tiles, caches the fastest in
+    tile_ir_MxNxK.json with the reference's keys, answers the next call from
+    that file, reads a file in the reference's own layout, and the tuned spec
+    computes the product through the tile_ir dispatch path."""
+    t0.GemmTuner(cache_dir=str(tmp_path), max_candidates=4, n_iters=3)
+    m, n, k = 256, 384, 512
+    r = t0.tune_tile_ir(rt, m, n, k)
+    assert not r.from_cache and r.best_tflops > 0 and len(r.all) >= 5, r
+    tfs = [tf for _, tf in r.all]
+    assert tfs == sorted(tfs, reverse=True)
+    assert r.all[0][0] == r.best.name() and r.all[0][1] == r.best_tflops
+    assert {t0.TileGemm.make(128, 128, 64).name(), t0.TileGemm.make(32, 64, 16).name()} <= {nm for nm, _ in r.all}
+    text = (tmp_path / f"tile_ir_{m}x{n}x{k}.json").read_text()
+    for key in ('"tile_m":', '"tile_n":', '"tile_k":', '"split_k":1', '"wgp":false', '"tflops":', '"all":[["',
+                '"arch":"gfx950"'):
+        assert key in text, (key, text)
+    r2 = t0.tune_tile_ir(rt, m, n, k)
+    assert r2.from_cache and r2.all == [] and r2.best.name() == r.best.name()
+    assert r2.best.waves_per_wg == r.best.waves_per_wg and abs(r2.best_tflops - r.best_tflops) < 0.01
+    # as the reference writes it: no arch, no wave count (the tile's gfx950 kernel is taken)
+    (tmp_path / "tile_ir_128x128x256.json").write_text(
+        '{"tile_m":64,"tile_n":64,"tile_k":16,"split_k":1,"wgp":false,"tflops":12.50,"all":[["x",12.50]]}')
+    r3 = t0.tune_tile_ir(rt, 128, 128, 256)
+    assert r3.from_cache and (r3.best.tile_m, r3.best.tile_n, r3.best.tile_k) == (64, 64, 16)
+    assert r3.best_tflops == 12.5 and r3.best.waves_per_wg >= 1
+    x = orc.xorshift_bf16(m * k, 3).reshape(m, k)
+    wt = orc.xorshift_bf16(n * k, 4).reshape(n, k)
+    kern = rt.ensure_tile_kernel(r.best)
+    dy = dev.zeros(m * n * 4)
+    rt.dispatch(kern, r.best.compute_grid(m, n), r.best.build_kernargs_m(dev.up(x), dev.up(wt), dy, k, n, m))
+    check_close(dev.down(dy, np.float32, m * n).reshape(m, n), orc.gemm_nt(x, wt), tolerance(f32(x), f32(wt), k),
+                r.best.name())
+
+
 # ------------------------------------------------------------------ graphs --
 
 def test_graph_pins_workspace():
