@@ -481,6 +481,27 @@ def test_tuner_and_auto_gemm(rt, dev, tmp_path):
                 "auto_gemm")
 
 
+def test_empty_and_malformed_calls_fail_before_launch(rt, dev):
+    """Empty or malformed problems return an error with a message before
+    anything is launched, and the runtime stays usable: the reference's
+    Result<_, String> paths (gemm_gen.rs:271-281, quant_kernels.rs:251-287)
+    rather than a fault or a poisoned runtime."""
+    buf = dev.zeros(64 * 64 * 4)
+    for m, n, k in ((0, 64, 64), (64, 0, 64), (64, 64, 0)):
+        for tr in (t0.NT, t0.NN):
+            with pytest.raises(t0.T0Error, match="empty GEMM"):
+                rt.gemm(buf, buf, buf, m, n, k, transpose=tr, out_dtype=t0.OUT_BF16)
+    with pytest.raises(t0.T0Error, match="split_k"):
+        rt.gemm(buf, buf, buf, 64, 64, 64, cfg=t0.GemmConfig.tile_128x128_k64().copy(split_k=3))
+    for k, gs in ((100, 128), (128, 12), (130, 64)):   # K % gs, gs % 8, K % 8
+        with pytest.raises(t0.T0Error):
+            rt.w4a16(buf, buf, buf, 0, buf, 4, 64, k, group_size=gs)
+    assert not rt.is_poisoned()
+    a = bf16(np.arange(64 * 64).reshape(64, 64) % 5 - 2)
+    got = run_gemm(rt, dev, a, a, 64, 64, 64, t0.NN, t0.OUT_F32)
+    assert np.array_equal(got, orc.gemm_nn(a, a))
+
+
 def test_tune_tile_ir(rt, dev, tmp_path):
     """src/t0/cost_model.rs:855-1150: tune_tile_ir times the reference's
     presets and the cost model's tiles, caches the fastest in
