@@ -16,6 +16,18 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 namespace t0 {
 
+// Compile-time loop: f(Idx<B>{}), ..., f(Idx<E-1>{}).  Register arrays
+// indexed through it stay in registers (a runtime index, even one an unrolled
+// loop makes constant, can leave them in scratch once lambdas are involved).
+template <int I> struct Idx { static constexpr int value = I; };
+template <int B, int E, class F>
+T0_DEV void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(Idx<B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
 // ---------------------------------------------------------------- buffers --
 // Raw buffer resource (gfx9 word3 = 0x00020000).  Out-of-range offsets
 // (>= num_records) read as zero; kernels use OOB_OFFSET to mask lanes.

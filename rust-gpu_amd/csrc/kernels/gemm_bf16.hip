@@ -480,7 +480,115 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
         }
     }
 
-    if constexpr (!PP) {
+    // ---- lean K loop (8 waves, two stages, interior tile, whole 64-k steps) ---
+    // The schedule of the loop below without its edge cases: waves 0-3 issue
+    // every DMA of a stage right after the step's barrier, each sub-step reads
+    // the next sub-step's fragments one per MFMA, the last step is peeled.
+    // With no K-tail or bounds branch in the body, the operand registers keep
+    // one assignment across the loop back-edge (no register copies), which
+    // takes ~8 % of the shader cycles off 4096^3 (147.7k against 160.5k per
+    // workgroup on one box).  Bit-identical to the general loop: the same
+    // MFMAs accumulate in the same order.
+    constexpr bool LEAN = PAIR_DMA && !PP && KK == 4;
+    bool lean = false;
+    if constexpr (LEAN) lean = pair_dma && k_len % BK == 0 && nk >= 2;
+    if constexpr (LEAN) {
+        if (lean) {
+            constexpr uint32_t HA = G::NW / 2 * G::A_LOADS * 1024, HB = G::NW / 2 * G::B_LOADS * 1024;
+            // waves 0-3: their chunks of stage t and those of wave + 4
+            auto lean_issue = [&](uint32_t t) {
+                if (wave < G::NW / 2) {
+                    const uint32_t kt = t * BK;
+                    const uint32_t st = lds_base + (t & 1) * G::STAGE_BYTES;
+                    const __amdgpu_buffer_rsrc_t ra = make_rsrc(A0 + (size_t)kt * 2);
+                    const __amdgpu_buffer_rsrc_t ra2 = make_rsrc(A0 + (size_t)kt * 2 + (size_t)(BM / 2) * lda * 2);
+                    const __amdgpu_buffer_rsrc_t rb = make_rsrc(NN ? B0 + (size_t)kt * ldb * 2 : B0 + (size_t)kt * 2);
+                    const __amdgpu_buffer_rsrc_t rb2 = make_rsrc(NN ? B0 + (size_t)(kt + BK / 2) * ldb * 2
+                                                                    : B0 + (size_t)kt * 2 + (size_t)(BN / 2) * ldb * 2);
+#pragma unroll
+                    for (int j = 0; j < G::A_LOADS; j++) {
+                        dma_x4(ra, __builtin_amdgcn_readfirstlane(st + (wave * G::A_LOADS + j) * 1024), ld.a_off[j]);
+                        dma_x4(ra2, __builtin_amdgcn_readfirstlane(st + HA + (wave * G::A_LOADS + j) * 1024), ld.a_off[j]);
+                    }
+#pragma unroll
+                    for (int j = 0; j < G::B_LOADS; j++) {
+                        dma_x4(rb, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + (wave * G::B_LOADS + j) * 1024),
+                               ld.b_off[j]);
+                        dma_x4(rb2, __builtin_amdgcn_readfirstlane(st + G::A_BYTES + HB + (wave * G::B_LOADS + j) * 1024),
+                               ld.b_off[j]);
+                    }
+                }
+            };
+            constexpr int BH = NN ? 2 : 1;                   // LDS reads per B fragment
+            constexpr int NQ = G::FM * G::FN;                // MFMAs per sub-step
+            constexpr int NR = G::FM + BH * G::FN;           // fragment reads per sub-step
+            bf16x8_t la[2][G::FM];
+            bf16x4_t lb[2][G::FN][2];                        // NN: the two transposing halves
+            bf16x8_t lbt[2][G::FN];                          // NT
+            // read q of sub-step KK_'s fragments into buffer BUF
+            auto lean_read = [&](const LDS_AS uint8_t* sa, auto KKc, auto BUFc, auto Qc) {
+                constexpr int kk = decltype(KKc)::value, buf = decltype(BUFc)::value, q = decltype(Qc)::value;
+                const LDS_AS uint8_t* sb = sa + G::A_BYTES;
+                if constexpr (q < G::FM) {
+                    la[buf][q] = *(const LDS_AS bf16x8_t*)(sa + a_kk[kk] + q * 32 * (BK * 2));
+                } else if constexpr (NN) {
+                    constexpr int j = (q - G::FM) / 2, h = (q - G::FM) % 2;
+                    lb[buf][j][h] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                        (LDS_AS bf16x4_t*)(sb + b_col[j] + kk * 16 * (BN * 2) + h * 4 * (BN * 2)));
+                } else {
+                    constexpr int j = q - G::FM;
+                    lbt[buf][j] = *(const LDS_AS bf16x8_t*)(sb + b_kk[kk] + j * 32 * (BK * 2));
+                }
+            };
+            auto lean_mfma = [&](auto BUFc, auto Qc) {
+                constexpr int buf = decltype(BUFc)::value, q = decltype(Qc)::value;
+                constexpr int i = q / G::FN, j = q % G::FN;
+                bf16x8_t b;
+                if constexpr (NN) b = __builtin_shufflevector(lb[buf][j][0], lb[buf][j][1], 0, 1, 2, 3, 4, 5, 6, 7);
+                else b = lbt[buf][j];
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, la[buf][i], acc[i][j], 0, 0, 0);
+            };
+            // NQ MFMAs from buffer CUR, the reads of (sa_next, KKN) into CUR ^ 1 one per MFMA
+            auto lean_sub = [&](auto CURc, const LDS_AS uint8_t* sa_next, auto KKNc, auto READc) {
+                constexpr int cur = decltype(CURc)::value;
+                constexpr bool rd = decltype(READc)::value != 0;
+                static_for<0, (NR > NQ ? NR : NQ)>([&](auto Q) {
+                    constexpr int q = decltype(Q)::value;
+                    if constexpr (rd && q < NR) lean_read(sa_next, KKNc, Idx<cur ^ 1>{}, Q);
+                    if constexpr (q < NQ) lean_mfma(CURc, Q);
+                });
+                static_for<0, (NR < NQ ? NR : NQ)>([&](auto) {
+                    if constexpr (rd) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                    // MFMA
+                });
+            };
+            lean_issue(0);
+            lean_issue(1);
+            wait_vmcnt<G::A_LOADS * 2 + G::B_LOADS * 2>();   // stage 0 landed (waves 0-3)
+            y_split_stride = p.y_split_stride;
+            asm volatile("" : "+s"(y_split_stride));
+            __syncthreads();
+            static_for<0, NR>([&](auto Q) { lean_read(stage_ptr(0), Idx<0>{}, Idx<0>{}, Q); });
+            for (uint32_t t = 0; t + 1 < nk; t++) {
+                const LDS_AS uint8_t* sa = stage_ptr(t);
+                lean_sub(Idx<0>{}, sa, Idx<1>{}, Idx<1>{});
+                lean_sub(Idx<1>{}, sa, Idx<2>{}, Idx<1>{});
+                lean_sub(Idx<0>{}, sa, Idx<3>{}, Idx<1>{});
+                // stage t + 1 landed in every wave, buffer t % 2 read by all
+                wait_vmcnt<0>();
+                __syncthreads();
+                if (t + 2 < nk) lean_issue(t + 2);
+                lean_sub(Idx<1>{}, stage_ptr(t + 1), Idx<0>{}, Idx<1>{});
+            }
+            const LDS_AS uint8_t* sa = stage_ptr(nk - 1);
+            lean_sub(Idx<0>{}, sa, Idx<1>{}, Idx<1>{});
+            lean_sub(Idx<1>{}, sa, Idx<2>{}, Idx<1>{});
+            lean_sub(Idx<0>{}, sa, Idx<3>{}, Idx<1>{});
+            lean_sub(Idx<1>{}, sa, Idx<0>{}, Idx<0>{});
+        }
+    }
+
+    if constexpr (!PP) { if (!lean) {
     // prologue: every buffer, then stage 0 visible and its first fragments
 #pragma unroll
     for (int s = 0; s < STAGES; s++)
@@ -552,7 +660,7 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
             }
         }
     }
-    }   // !PP
+    } }   // !PP, !lean
 
     // ---- epilogue -----------------------------------------------------------
     // acc[i][j][r] holds C[m0 + wm*TM + i*32 + lane%32][n0 + wn*TN + j*32 + 8*(r/4) + 4*(lane/32) + r%4].
