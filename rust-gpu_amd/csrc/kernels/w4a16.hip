@@ -62,7 +62,9 @@ T0_DEV void store_out4(const t0_w4a16_params& p, uint32_t m, uint32_t n, f32x4_t
 //     S, Z -> the same slot by 4-byte DMAs: the group's scales of columns
 //        [c0, c1) and the zero-point words holding them
 //   Groups go in rounds of SLOTS (up to 4, as LDS and registers allow): every load of the
-//   round is issued, group by group, before the first group is consumed.
+//   round is issued before the first group is consumed, the weight loads of
+//   all the round's groups first (they come from HBM; the activations, read
+//   by every workgroup, from L2), then group by group the LDS loads.
 //   Each group issues a fixed number of loads, so an explicit vmcnt wait
 //   lets a group's LDS data be read while the later groups' loads are still
 //   in flight; the DMAs are compiler-visible (buffer-load-to-LDS builtin), so
@@ -141,7 +143,10 @@ __device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, LDS_AS 
     const uint32_t c = lane & 15, h = lane >> 4;
     constexpr uint32_t ES = SF32 ? 4 : 2;               // scale bytes
     // VMEM ops per group: A (DMA blocks, or residual / hidden / gamma pairs), S, Z, W
-    constexpr int GROUP_LOADS = (NORM ? 3 : G::A_DMA) + 1 + (ZP ? 1 : 0) + TILES;
+    // Without the norm, every weight load of the round goes out first (the
+    // weights come from HBM, the activations from L2), so between two groups'
+    // LDS loads there are only LDS loads: A, S, Z.
+    constexpr int GROUP_LOADS = (NORM ? 3 : G::A_DMA) + 1 + (ZP ? 1 : 0) + (NORM ? TILES : 0);
 
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A);
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.scales);
@@ -192,12 +197,24 @@ __device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, LDS_AS 
     const uint32_t nj = GP > wave ? (GP - wave + G::WAVES - 1) / G::WAVES : 0;
 #pragma unroll 1
     for (uint32_t j0 = 0; j0 < nj; j0 += G::SLOTS) {
-        // ---- 1. every load of the round, group by group ----------------------
+        // ---- 1. every load of the round: the weights of all its groups, then
+        // each group's activations, scales and zero points --------------------
         u32x4_t wq[G::SLOTS][TILES];
         u32x2_t nr[G::SLOTS], nh[G::SLOTS], ng[G::SLOTS];   // NORM: residual, hidden, gamma pairs
+        if constexpr (!NORM) {
+#pragma unroll
+            for (int s = 0; s < G::SLOTS; s++) {
+                const bool ok = j0 + s < nj;      // wave-uniform; a group past nj reads zeros and adds 0
+                const uint32_t g = g_begin + wave + G::WAVES * (j0 + s);
+#pragma unroll
+                for (int t = 0; t < TILES; t++)
+                    wq[s][t] = buffer_load_x4(rw, ok && w_row[t] != OOB_OFFSET ? w_row[t] + g * 64 : OOB_OFFSET);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
 #pragma unroll
         for (int s = 0; s < G::SLOTS; s++) {
-            const bool ok = j0 + s < nj;          // wave-uniform; a group past nj reads zeros and adds 0
+            const bool ok = j0 + s < nj;
             const uint32_t g = g_begin + wave + G::WAVES * (j0 + s);
             LDS_AS uint8_t* dst = slot[s] + wave * G::WAVE_SLOT;
             if constexpr (NORM) {
@@ -218,9 +235,11 @@ __device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, LDS_AS 
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rz, (lds_void*)(dst + G::Z_OFF), 4,
                                                         ok && z_lane != OOB_OFFSET ? z_lane + g * (N / 8) * 4 : OOB_OFFSET,
                                                         0, 0, 0);
+            if constexpr (NORM) {
 #pragma unroll
-            for (int t = 0; t < TILES; t++)
-                wq[s][t] = buffer_load_x4(rw, ok && w_row[t] != OOB_OFFSET ? w_row[t] + g * 64 : OOB_OFFSET);
+                for (int t = 0; t < TILES; t++)
+                    wq[s][t] = buffer_load_x4(rw, ok && w_row[t] != OOB_OFFSET ? w_row[t] + g * 64 : OOB_OFFSET);
+            }
             __builtin_amdgcn_sched_barrier(0);   // keep the groups' loads in consumption order
         }
         // ---- 2. consume the groups in order: a group's LDS data is complete
