@@ -642,7 +642,10 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
 #pragma unroll
             for (int i = 0; i < G::FM; i++) correction(i);
         }
-        for (uint32_t t = 0; t < nk; t++) {
+        // One step; N2 / N1: stage t + 2 is to be loaded / step t + 1 exists.
+        // The last two steps are peeled, so the loop body has no such branch.
+        auto step = [&](uint32_t t, auto N2c, auto N1c) {
+            constexpr bool has2 = decltype(N2c)::value != 0, has1 = decltype(N1c)::value != 0;
             const LDS_AS uint8_t* sa = stage_at(t);
 #pragma unroll
             for (int kk = 0; kk < 8; kk++) {
@@ -657,15 +660,17 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
                     __builtin_amdgcn_sched_barrier(0);
                     asm volatile("" ::: "memory");
                 }
-                if (kk >= 4 && t + 2 < nk) {
+                if constexpr (has2) {
+                    if (kk >= 4) {
 #pragma unroll
-                    for (int q = (kk - 4) * PER; q < (kk - 3) * PER && q < NQ; q++) issue_q(t + 2, q);
+                        for (int q = (kk - 4) * PER; q < (kk - 3) * PER && q < NQ; q++) issue_q(t + 2, q);
+                    }
                 }
                 if (kk + 1 < 8) {
 #pragma unroll
                     for (int i = 0; i < G::FM; i++)
                         af[cur ^ 1][i] = *(const LDS_AS bf16x8_t*)(sa + a_lo[kk + 1] + i * 32 * 256);
-                } else if (t + 1 < nk) {
+                } else if constexpr (has1) {
                     read_first(stage_at(t + 1), af[cur ^ 1], wlo_n, whi_n, zw_n, xr_n);
                 }
                 // the next sub-step's reads stay ahead of this one's MFMAs
@@ -708,7 +713,11 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
                 correction(i);   // after the last group: unused, on the last group's operands
             }
             __builtin_amdgcn_sched_barrier(0);
-        }
+        };
+        uint32_t t = 0;
+        for (; t + 2 < nk; t++) step(t, Idx<1>{}, Idx<1>{});
+        if (t + 1 < nk) step(t++, Idx<0>{}, Idx<1>{});
+        if (t < nk) step(t, Idx<0>{}, Idx<0>{});
     } else {
 #pragma unroll
     for (int s = 0; s < STAGES - 1; s++)
