@@ -235,14 +235,19 @@ def test_w4a16_prefill_f32_scales(rt, dev, m, n):
     check_close(got32, ref, w4_tol(a, qw, s, zw, 0, n, k, gs), f"prefill f32 scales {m}x{n}")
 
 
-@pytest.mark.parametrize("per_group_zeros", [True, False])
-def test_w4a16_prefill_exact_integers(rt, dev, per_group_zeros):
+@pytest.mark.parametrize("per_group_zeros,m,k", [(True, 320, 512), (False, 320, 512),
+                                                 (True, 1024, 128), (True, 1024, 256), (False, 1024, 384),
+                                                 (True, 1024, 1152)])
+def test_w4a16_prefill_exact_integers(rt, dev, per_group_zeros, m, k):
     """Integer activations in [-3, 3] and power-of-two scales: every group's
     sum a*(q - z) is an integer below 2^13 and the scaled sum over groups is
     exact in f32, so the f32 output must equal the exact product bit for bit
-    (the zero-point term enters as one more MFMA block of row sums)."""
-    rng = np.random.default_rng(71 + per_group_zeros)
-    m, n, k, gs = 320, 256, 512, 128
+    (the zero-point term enters as one more MFMA block of row sums).  M = 320
+    runs the two-stage 128x128 tiles; M = 1024 the three-stage 128x256 tiles,
+    over 1, 2, 3 and 9 quant groups (the peeled last steps alone, and with
+    the loop)."""
+    rng = np.random.default_rng(71 + per_group_zeros + m + k)
+    n, gs = 256, 128
     G = k // gs
     qw, _, zw = make_w4(rng, n, k, gs, per_group_zeros=per_group_zeros)
     s = bf16(2.0 ** rng.integers(-8, -4, (G, n)).astype(np.float32))
@@ -257,7 +262,7 @@ def test_w4a16_prefill_exact_integers(rt, dev, per_group_zeros):
     w = (q - np.repeat(z.T, gs, axis=1)) * np.repeat(f32(s).astype(np.float64).T, gs, axis=1)   # [n, k]
     ref = (ai.astype(np.float64) @ w.T).astype(np.float32)
     plan, _ = rt.w4a16_plan(0, 0, 0, 0, 0, m, n, k, group_size=gs)
-    assert plan.startswith("t0k_w4a16_prefill")
+    assert plan.startswith("t0k_w4a16_prefill") and ("_s3" in plan) == (m >= 1024), plan
     got = run_w4(rt, dev, a, qw, s, zw, m, n, k, gs, zc=zc, out_f32=True)
     assert np.array_equal(got, ref)
 
