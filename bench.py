@@ -284,6 +284,7 @@ def bench_gemm_4096(rt, steps, warmup, rng, tr):
                                   out_dtype=t0.OUT_BF16, cfg=cfg) for _ in range(5)]
     sclk = float(np.median([p[0] for p in probes]))
     span = float(np.median([p[1] for p in probes]))
+    wg_cycles = float(np.median([p[2] for p in probes]))
     flops = 2.0 * m * n * k
     tflops = flops / (ms * 1e-3) / 1e12
     step()
@@ -293,6 +294,8 @@ def bench_gemm_4096(rt, steps, warmup, rng, tr):
         buf.free()
     rf = roofline("mfma", tflops, PEAK_TFLOPS, "TFLOP/s", traffic_of(tr, "gemm_4096_nn_bf16"))
     rf["sclk_mhz_measured"] = round(sclk, 1)
+    # the shader cycles a workgroup takes (MFMA issue alone: 131072 per SIMD)
+    rf["workgroup_cycles_measured"] = round(wg_cycles)
     rf["peak_at_measured_sclk"] = round(PEAK_TFLOPS * sclk / 2400.0, 1)
     rf["frac_at_measured_sclk"] = round(tflops / (PEAK_TFLOPS * sclk / 2400.0), 4)
     return {"ms": ms, "ms_median_per_launch": float(np.median(per)), "tflops": tflops, "kernel": cfg.name(),

@@ -311,12 +311,13 @@ int t0_gemm_select(t0_runtime* rt, const t0_gemm_desc* d, t0_gemm_config* out);
 /* Measurement aid with no counterpart in the reference (its README quotes
  * the nominal clock only): runs t0_gemm once with per-workgroup timestamps
  * (shader clock and the 100 MHz real-time clock at each workgroup's start and
- * end), waits, and returns the median shader clock over workgroups in MHz and
- * the span from the first start to the last end in microseconds.  Tiled
+ * end), waits, and returns the median shader clock over workgroups in MHz,
+ * the span from the first start to the last end in microseconds and (when
+ * wg_cycles is not NULL) the median shader cycles per workgroup.  Tiled
  * kernels without split-K only (else T0_ERR_INVALID); at most 65536
  * workgroups.  Synchronous. */
 int t0_gemm_clock_probe(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm_desc* d, double* sclk_mhz,
-                        double* span_us);
+                        double* span_us, double* wg_cycles);
 /* No counterpart in the reference: t0_gemm for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc).  Same arguments and results as t0_gemm; the

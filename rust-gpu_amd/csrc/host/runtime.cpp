@@ -1043,7 +1043,7 @@ int t0_gemm(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm_desc* d) {
 }
 
 int t0_gemm_clock_probe(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm_desc* d, double* sclk_mhz,
-                        double* span_us) {
+                        double* span_us, double* wg_cycles) {
     if (!rt || !d || !sclk_mhz || !span_us) return fail(T0_ERR_INVALID, "null argument");
     std::lock_guard<std::recursive_mutex> call_lock(rt->call_mu);
     const size_t max_wg = 65536;
@@ -1058,19 +1058,22 @@ int t0_gemm_clock_probe(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm
     std::vector<uint64_t> ts((size_t)wgs * 4);
     HIPCHK(hipStreamSynchronize(rt->stream));
     HIPCHK(hipMemcpy(ts.data(), rt->probe, ts.size() * 8, hipMemcpyDeviceToHost));
-    std::vector<double> mhz;
+    std::vector<double> mhz, cyc;
     uint64_t first = ~0ull, last = 0;
     for (uint32_t w = 0; w < wgs; w++) {
         const uint64_t rt0 = ts[4 * w], rt1 = ts[4 * w + 1], c0 = ts[4 * w + 2], c1 = ts[4 * w + 3];
         if (rt1 <= rt0) continue;
         mhz.push_back((double)(c1 - c0) / (double)(rt1 - rt0) * 100.0);   // s_memrealtime counts at 100 MHz
+        cyc.push_back((double)(c1 - c0));
         first = std::min(first, rt0);
         last = std::max(last, rt1);
     }
     if (mhz.empty()) return fail(T0_ERR_HIP, "clock probe: no workgroup recorded its timestamps");
     std::sort(mhz.begin(), mhz.end());
+    std::sort(cyc.begin(), cyc.end());
     *sclk_mhz = mhz[mhz.size() / 2];
     *span_us = (double)(last - first) / 100.0;
+    if (wg_cycles) *wg_cycles = cyc[cyc.size() / 2];
     return T0_OK;
 }
 

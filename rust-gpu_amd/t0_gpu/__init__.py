@@ -416,12 +416,12 @@ class GpuRuntime:
     def gemm_clock_probe(self, a: int, b: int, c: int, m: int, n: int, k: int, transpose=NT, out_dtype=OUT_F32,
                          cfg: GemmConfig | None = None):
         """One GEMM with per-workgroup timestamps: (median shader clock in MHz,
-        first-start to last-end span in us)."""
+        first-start to last-end span in us, median shader cycles per workgroup)."""
         d = GemmDescC(a=a, b=b, c=c, m=m, n=n, k=k, transpose=transpose, out_dtype=out_dtype)
-        mhz, span = C.c_double(), C.c_double()
+        mhz, span, cyc = C.c_double(), C.c_double(), C.c_double()
         _check(lib().t0_gemm_clock_probe(self.h, C.byref(cfg) if cfg is not None else None, C.byref(d),
-                                         C.byref(mhz), C.byref(span)))
-        return mhz.value, span.value
+                                         C.byref(mhz), C.byref(span), C.byref(cyc)))
+        return mhz.value, span.value, cyc.value
 
     def gemm_select(self, m, n, k, transpose=NT, out_dtype=OUT_F32) -> GemmConfig:
         d = GemmDescC(m=m, n=n, k=k, transpose=transpose, out_dtype=out_dtype)

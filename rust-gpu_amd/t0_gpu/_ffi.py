@@ -135,7 +135,7 @@ SIGNATURES = {
     "t0_tuner_cache_load": ([u32, u32, u32, u32, u32, P(GemmConfigC), P(f64)], C.c_int),
     "t0_tuner_invalidate": ([u32, u32, u32, u32, u32], C.c_int),
     "t0_gemm_noalloc": ([vp, P(GemmConfigC), P(GemmDescC)], C.c_int),
-    "t0_gemm_clock_probe": ([vp, P(GemmConfigC), P(GemmDescC), P(f64), P(f64)], C.c_int),
+    "t0_gemm_clock_probe": ([vp, P(GemmConfigC), P(GemmDescC), P(f64), P(f64), P(f64)], C.c_int),
     "t0_gemm_select": ([vp, P(GemmDescC), P(GemmConfigC)], C.c_int),
     "t0_tune": ([vp, u32, u32, u32, u32, u32, P(GemmConfigC), P(f64)], C.c_int),
     "t0_tuner_set_cache_dir": ([cp], C.c_int),
