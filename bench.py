@@ -186,7 +186,35 @@ def bench_ceilings(rt, steps, warmup, rng):
     out["lds_bytes_per_clk_per_cu"] = rates
     for b in ops + [rec, src64]:
         b.free()
+    out["gemm_4096_zero_operands"] = bench_gemm_zero_operands(rt, steps, warmup)
     return out
+
+
+def bench_gemm_zero_operands(rt, steps, warmup):
+    """Not a BASELINE workload: the headline GEMM (the same config, kernel and
+    schedule) on all-zero A and B.  Only the operand values differ from the
+    N(0,1) run, so the gap in clock and time is what the MFMAs' data-dependent
+    power costs the GEMM."""
+    m = n = k = 4096
+    da, db, dc = rt.alloc(m * k * 2), rt.alloc(k * n * 2), rt.alloc(m * n * 2)
+    rt.memset(da.gpu_addr(), 0, m * k * 2)
+    rt.memset(db.gpu_addr(), 0, k * n * 2)
+    cfg = rt.gemm_select(m, n, k, t0.NN, t0.OUT_BF16)
+
+    def step():
+        rt.gemm(da.gpu_addr(), db.gpu_addr(), dc.gpu_addr(), m, n, k, transpose=t0.NN, out_dtype=t0.OUT_BF16,
+                cfg=cfg)
+
+    ms = Timer(rt).run(step, steps, warmup)
+    probes = [rt.gemm_clock_probe(da.gpu_addr(), db.gpu_addr(), dc.gpu_addr(), m, n, k, transpose=t0.NN,
+                                  out_dtype=t0.OUT_BF16, cfg=cfg) for _ in range(5)]
+    for buf in (da, db, dc):
+        buf.free()
+    tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+    return {"kernel": cfg.name(), "us_per_launch": round(ms * 1e3, 2), "tflops": round(tflops, 1),
+            "frac_of_peak": round(tflops / PEAK_TFLOPS, 4),
+            "sclk_mhz": round(float(np.median([p[0] for p in probes])), 1),
+            "workgroup_cycles": round(float(np.median([p[2] for p in probes])))}
 
 
 TILE_SHAPES = [(m, n, k) for m in (32, 128, 512, 1024, 2048, 4096)
