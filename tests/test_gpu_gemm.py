@@ -195,6 +195,48 @@ def test_eight_wave_256_tiles(rt, dev, m, n, k):
             assert np.array_equal(got16, f32(orc.bf16_rne(want.astype(np.float32)))), (cfg.name(), m, n, k, layout)
 
 
+@pytest.mark.parametrize("sk", [1, 2, 4])
+def test_eight_wave_256x64_split_k_and_bias(rt, dev, sk):
+    """The 8-wave 256x256x64 instance on interior tiles with whole 64-k steps
+    per partition (its branch-free K loop) and on edge tiles (the general
+    loop) in one launch, bit-exact on small-integer operands: split-K
+    reduced in-kernel (bf16 out, NN and NT), f32 planes summed on the host
+    through the gemm_gen dispatch, and the bias + ReLU epilogue with integer
+    bias values."""
+    rng = np.random.default_rng(500 + sk)
+    k = 1024                                  # K / split_k = 1024, 512 or 256: whole 64-k steps
+    cfg0 = t0.GemmConfig.tile_256x256_k64().copy(wg_size=512)
+    for m, n in ((512, 512), (300, 520)):     # all tiles interior / interior and edge tiles
+        ai = rng.integers(-8, 9, size=(m, k))
+        bi = rng.integers(-6, 7, size=(k, n))
+        want = ai.astype(np.int64) @ bi.astype(np.int64)
+        a, b = bf16(ai), bf16(bi)
+        for layout, bb in ((t0.NN, b), (t0.NT, bf16(bi.T.copy()))):
+            cfg = cfg0.copy(transpose=layout, out_dtype=t0.OUT_BF16, split_k=sk if sk > 1 else 0)
+            got16 = run_gemm(rt, dev, a, bb, m, n, k, layout, t0.OUT_BF16, cfg=cfg)
+            assert np.array_equal(got16, f32(orc.bf16_rne(want.astype(np.float32)))), (sk, m, n, layout)
+        if m % 256:
+            continue                          # the gemm_gen grid has M / tile_m tiles
+        da, db = dev.up(a), dev.up(b)
+        if sk > 1:
+            cfg = cfg0.copy(transpose=t0.NN, out_dtype=t0.OUT_F32, split_k=sk)
+            planes = dev.zeros(sk * m * n * 4)
+            kern = rt.ensure_kernel_t0(cfg)
+            gx, gy = t0.compute_grid_auto(cfg, m, n)
+            rt.dispatch(kern, [gx, gy, 1], t0.build_kernargs(da, db, planes, k, n, m, cfg))
+            got = orc.splitk_sum(dev.down(planes, np.float32, sk * m * n).reshape(sk, m, n))
+            assert np.array_equal(got.astype(np.int64), want), sk
+        else:
+            bias = rng.integers(-300, 301, size=n).astype(np.float32)
+            cfg = cfg0.copy(transpose=t0.NN, out_dtype=t0.OUT_F32, epilogue=t0.EPI_BIAS_ADD_RELU)
+            dy = dev.zeros(m * n * 4)
+            kern = rt.ensure_kernel_t0(cfg)
+            gx, gy = t0.compute_grid_auto(cfg, m, n)
+            rt.dispatch(kern, [gx, gy, 1], t0.build_kernargs_with_bias(da, db, dy, k, n, m, cfg, dev.up(bias)))
+            got = dev.down(dy, np.float32, m * n).reshape(m, n)
+            assert np.array_equal(got.astype(np.int64), np.maximum(want + bias.astype(np.int64), 0))
+
+
 # ----------------------------------------------------------------- bounds --
 
 @pytest.mark.parametrize("m,n,k", [(33, 31, 40), (1, 1, 8), (255, 257, 264), (100, 200, 72), (300, 130, 1000)])
