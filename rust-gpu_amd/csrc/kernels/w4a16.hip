@@ -120,9 +120,9 @@ struct W4DecCfg {
     static constexpr int MAX_GROUP_LOADS = A_DMA + 2 + TILES;   // VMEM ops per group: A, S, Z, W
     static_assert(SLOTS * MAX_GROUP_LOADS < 64, "vmcnt range");
     static_assert(SLOTS >= 1 && SLOTS * SLOT_BYTES <= 156 * 1024, "LDS");
-    static_assert(WAVES * OUT_SLOTS * 16 <= SLOT_BYTES, "reduction fits slot 0");
     static_assert(TILES <= 4, "scale / zero-point DMA covers 64 columns");
-    static_assert(WAVES * OUT_SLOTS * 16 + WAVES * 4 <= SLOT_BYTES, "wave sums of squares after the partials");
+    static_assert(OUT_SLOTS * 16 + 4 <= WAVE_SLOT && WAVE_SLOT % 16 == 0,
+                  "a wave's partials and sum of squares fit its own slot-0 area");
 };
 
 template <int TILES, int MB, bool ZP, bool SF32, bool NORM>
@@ -319,20 +319,22 @@ __device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, LDS_AS 
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) ssq += __shfl_xor(ssq, o, 64);
     }
-    __syncthreads();                                     // LDS free for the reduction
+    // Each wave parks its partials (and its sum of squares) in its own slot-0
+    // area, which only it has used, so no barrier is needed before the writes.
+    constexpr uint32_t RED_STRIDE = G::WAVE_SLOT / 16;   // f32x4 per wave area
     LDS_AS f32x4_t* red = (LDS_AS f32x4_t*)slot[0];
-    LDS_AS float* red_ssq = (LDS_AS float*)(slot[0] + G::WAVES * G::OUT_SLOTS * 16);
 #pragma unroll
     for (int t = 0; t < TILES; t++)
 #pragma unroll
-        for (int mb = 0; mb < MB; mb++) red[(wave * TILES * MB + t * MB + mb) * 64 + lane] = acc[t][mb];
-    if (NORM && lane == 0) red_ssq[wave] = ssq;
+        for (int mb = 0; mb < MB; mb++) red[wave * RED_STRIDE + (t * MB + mb) * 64 + lane] = acc[t][mb];
+    if (NORM && lane == 0) *(LDS_AS float*)(slot[0] + wave * G::WAVE_SLOT + G::OUT_SLOTS * 16) = ssq;
     __syncthreads();
     float inv_rms = 1.0f;
     if constexpr (NORM) {
-        float t = red_ssq[0];
+        float t = *(const LDS_AS float*)(slot[0] + G::OUT_SLOTS * 16);
 #pragma unroll
-        for (int q = 1; q < G::WAVES; q++) t += red_ssq[q];   // in wave order
+        for (int q = 1; q < G::WAVES; q++)   // in wave order
+            t += *(const LDS_AS float*)(slot[0] + q * G::WAVE_SLOT + G::OUT_SLOTS * 16);
         inv_rms = 1.0f / sqrtf(t / (float)K + p.norm_eps);
     }
     constexpr uint32_t TILE_BYTES = G::OUT_SLOTS * 16;
@@ -346,7 +348,7 @@ __device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, LDS_AS 
         if (slot < (uint32_t)G::OUT_SLOTS) {
             f32x4_t pw[G::WAVES];                        // every wave's partial in flight at once
 #pragma unroll
-            for (int q = 0; q < G::WAVES; q++) pw[q] = red[q * G::OUT_SLOTS + slot];
+            for (int q = 0; q < G::WAVES; q++) pw[q] = red[q * RED_STRIDE + slot];
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int q = 0; q < G::WAVES; q++) v[e] += pw[q];   // in wave order
