@@ -352,11 +352,28 @@ def bench_skinny(rt, steps, warmup, rng, tr):
     one(0)
     rt.wait_idle()
     out0 = dc.read(np.uint16, m * n).reshape(m, n)
+    # Operand read floors: the pick's grid (and two other tilings) with only the
+    # operand slices moving to LDS -- A, B, both -- on the same rotated B sets,
+    # and an empty launch of the pick's grid.
+    floors = {}
+    for label, c in (("pick", cfg), ("128x64_split4", cfg.copy(tile_m=128, tile_n=64, split_k=4)),
+                     ("128x128_split8", cfg.copy(tile_m=128, tile_n=128, split_k=8))):
+        row = {"tiling": f"{c.tile_m}x{c.tile_n} split {max(1, c.split_k)}"}
+        for mode, key in ((1, "A"), (2, "B"), (3, "A+B")):
+            ms_f, _ = rotate_timed(rt, lambda i: rt.floor_tile_read(da.gpu_addr(), bs[i].gpu_addr(), m, n, k,
+                                                                     transpose=t0.NN, mode=mode, cfg=c),
+                                   steps, warmup)
+            row[f"us_{key}"] = round(ms_f * 1e3, 3)
+        floors[label] = row
+    wgs = (m // cfg.tile_m) * (n // cfg.tile_n) * max(1, cfg.split_k)
+    ms_e, _ = rotate_timed(rt, lambda i: rt.floor_empty(wgs, cfg.wg_size), steps, warmup)
+    floors["pick"]["us_empty_launch"] = round(ms_e * 1e3, 3)
     for buf in bs + [da, dc]:
         buf.free()
     return {"workload": "skinny bf16 GEMM M=128 N=4096 K=4096 NN, bf16 out", "kernel": cfg.name(),
             "us_per_launch": round(ms * 1e3, 3), "us_median_per_launch": round(med * 1e3, 3),
             "tflops": round(tflops, 2), "gbs": round(gbs, 1), "_host": (a, b0, out0),
+            "operand_read_floor": floors,
             "roofline": roofline("hbm", gbs, PEAK_GBS, "GB/s", traffic_of(tr, "gemm_skinny_128x4096x4096"))}
 
 

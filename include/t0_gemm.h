@@ -445,6 +445,16 @@ int t0_copy_device(t0_runtime* rt, uint64_t src, uint64_t dst, uint64_t bytes);
 int t0_floor_stream_read(t0_runtime* rt, uint64_t src, uint64_t bytes, uint64_t sink, uint32_t workgroups,
                          uint32_t threads);
 int t0_floor_empty(t0_runtime* rt, uint32_t workgroups, uint32_t threads);
+/* Operand read floor of a GEMM tiling (measurement aid, no reference
+ * counterpart): one launch with the grid t0_gemm would use for cfg (NULL:
+ * t0_gemm_select's pick) on d's shape, in which every workgroup only moves
+ * its operand slices -- the A rows of its tile (mode 1), the B columns
+ * (mode 2) or both (mode 3) over its split-K partition -- from d->a / d->b to
+ * LDS, 64 k per step, as the GEMM stages them: no MFMAs, no partial sums, no
+ * stores.  The time the tiling's operand traffic takes on its own.  Tiled
+ * configs with tile_m, tile_n multiples of 8, tile_m + tile_n <= 512, K a
+ * multiple of 64 * split_k, operands under 4 GiB.  Asynchronous. */
+int t0_floor_tile_read(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm_desc* d, int mode);
 /* Ceilings of the compute-bound GEMM (measurement aids, no reference
  * counterpart).  t0_floor_mfma issues mfma_per_wave (a multiple of 16)
  * v_mfma_f32_32x32x16_bf16 per wave from registers on `workgroups` 512-thread

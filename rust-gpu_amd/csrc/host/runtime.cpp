@@ -1703,6 +1703,44 @@ int t0_floor_empty(t0_runtime* rt, uint32_t workgroups, uint32_t threads) {
     return launch(rt, f, workgroups, 1, 1, threads, p);
 }
 
+int t0_floor_tile_read(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm_desc* d, int mode) {
+    if (!rt || !d || !d->a || !d->b) return fail(T0_ERR_INVALID, "null argument");
+    if (mode < 1 || mode > 3) return fail(T0_ERR_INVALID, "mode 1 (A slices), 2 (B slices) or 3 (both)");
+    if (!d->m || !d->n || !d->k || d->transpose > T0_NN) return fail(T0_ERR_INVALID, "bad shape or layout");
+    t0_gemm_config c;
+    if (cfg) c = *cfg;
+    else {
+        int r = t0_gemm_select(rt, d, &c);
+        if (r) return r;
+    }
+    const uint32_t sk = split_of(c);
+    if (c.tile_m % 8 || c.tile_n % 8 || !c.tile_m || !c.tile_n || c.tile_m + c.tile_n > 512)
+        return fail(T0_ERR_INVALID, "tile_m and tile_n multiples of 8 with tile_m + tile_n <= 512");
+    if (d->k % (64 * sk)) return fail(T0_ERR_INVALID, "K must be a multiple of 64 * split_k");
+    const bool nt = d->transpose == T0_NT;
+    const uint64_t lda = d->lda ? d->lda : d->k, ldb = d->ldb ? d->ldb : (nt ? d->k : d->n);
+    if (lda < d->k || ldb < (nt ? d->k : d->n)) return fail(T0_ERR_INVALID, "leading dimension below the row length");
+    if ((uint64_t)d->m * lda * 2 >= (1ull << 32) || (uint64_t)(nt ? d->n : d->k) * ldb * 2 >= (1ull << 32))
+        return fail(T0_ERR_INVALID, "operands must stay under 4 GiB");
+    const uint64_t tiles = (uint64_t)((d->m + c.tile_m - 1) / c.tile_m) * ((d->n + c.tile_n - 1) / c.tile_n);
+    if (tiles * sk > 0x7FFFFFFFu) return fail(T0_ERR_INVALID, "too many workgroups");
+    int r = set_dev(rt);
+    if (r) return r;
+    hipFunction_t f;
+    r = get_fn(rt, "t0k_tile_read", &f);
+    if (r) return r;
+    t0_tile_read_params p;
+    memset(&p, 0, sizeof p);
+    p.A = (const void*)d->a;
+    p.B = (const void*)d->b;
+    p.M = d->m; p.N = d->n; p.K = d->k;
+    p.lda = (uint32_t)lda; p.ldb = (uint32_t)ldb;
+    p.tile_m = c.tile_m; p.tile_n = c.tile_n; p.split_k = sk;
+    p.b_nt = nt;
+    p.mode = (uint32_t)mode;
+    return launch(rt, f, (uint32_t)(tiles * sk), 1, 1, 256, p);
+}
+
 int t0_floor_mfma(t0_runtime* rt, uint64_t operands, uint64_t out, uint32_t workgroups, uint32_t mfma_per_wave) {
     if (!rt || !operands || !out || operands % 16 || out % 8) return fail(T0_ERR_INVALID, "null or misaligned buffer");
     if (!workgroups || !mfma_per_wave || mfma_per_wave % 16)

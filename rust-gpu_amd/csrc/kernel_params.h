@@ -134,6 +134,17 @@ typedef struct t0_aux_params {
     uint32_t aux_pad_;
 } t0_aux_params;
 
+// t0k_tile_read: the operand traffic of one GEMM tiling on its own (measurement aid).
+typedef struct t0_tile_read_params {
+    const void* A;        // bf16 [M, lda]
+    const void* B;        // bf16 [N, ldb] (b_nt) or [K, ldb]
+    uint32_t M, N, K;
+    uint32_t lda, ldb;
+    uint32_t tile_m, tile_n, split_k;
+    uint32_t b_nt;
+    uint32_t mode;        // bit 0: the A slices, bit 1: the B slices
+} t0_tile_read_params;
+
 // t0_aux_params.flags bit for the conversions: src 16-byte aligned, ld_src % 4 == 0.
 #define T0_AUX_SRC_VEC4 0x100u
 

@@ -340,6 +340,73 @@ extern "C" __global__ void __launch_bounds__(1024) t0k_stream_read(const t0_aux_
 }
 extern "C" __global__ void __launch_bounds__(1024) t0k_empty(const t0_aux_params p) {}
 
+// Operand read floor of a GEMM tiling.  Workgroup b takes the tile and K
+// partition the tiled GEMM kernels give it (xcd_remap, then grouped_tile with
+// groups of 4 tile rows) and moves its A slice (tile_m rows) and/or B slice
+// (tile_n columns) of the partition's k range to LDS by global->LDS DMA, 64 k
+// per step, the way the GEMM stages them, with nothing else: no fragment
+// reads, MFMAs or stores.  Up to 48 DMAs per lane are in flight.  The host
+// checks K % (64 * split_k) == 0, tile_m and tile_n multiples of 8 with
+// tile_m + tile_n <= 512 (at most 16 chunks of 16 bytes per lane and step),
+// and operands under 4 GiB.
+extern "C" __global__ void __launch_bounds__(256) t0k_tile_read(const t0_tile_read_params p) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[16 * 1024];
+    typedef __attribute__((address_space(3))) void lds_void;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t tiles_m = (p.M + p.tile_m - 1) / p.tile_m, tiles_n = (p.N + p.tile_n - 1) / p.tile_n;
+    const uint32_t tiles = tiles_m * tiles_n, total = tiles * p.split_k;
+    if (blockIdx.x >= total) return;
+    const uint32_t lid = t0::xcd_remap(blockIdx.x, total);
+    const uint32_t part = lid / tiles;
+    uint32_t tm, tn;
+    t0::grouped_tile(lid % tiles, tiles_m, tiles_n, 4, tm, tn);
+    const uint32_t m0 = tm * p.tile_m, n0 = tn * p.tile_n;
+    const uint32_t k_per = p.K / p.split_k, k0 = part * k_per, steps = k_per / 64;
+    const uint32_t ca = (p.mode & 1) ? 8 * p.tile_m : 0;     // 16-byte chunks of A per step
+    const uint32_t cs = ca + ((p.mode & 2) ? 8 * p.tile_n : 0);   // a multiple of 64
+    const uint32_t adv_b = p.b_nt ? 128 : 64 * p.ldb * 2;   // bytes per step
+    const __amdgpu_buffer_rsrc_t ra = t0::make_rsrc(p.A), rb = t0::make_rsrc(p.B);
+    // chunk j * 256 + tid of each step: its offset at step 0
+    uint32_t off[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        uint32_t q = j * 256 + tid, o = t0::OOB_OFFSET;
+        if (q < ca) {
+            const uint32_t row = m0 + (q >> 3);
+            if (row < p.M) o = row * p.lda * 2 + k0 * 2 + (q & 7) * 16;
+        } else if (q < cs) {
+            q -= ca;
+            if (p.b_nt) {
+                const uint32_t row = n0 + (q >> 3);
+                if (row < p.N) o = row * p.ldb * 2 + k0 * 2 + (q & 7) * 16;
+            } else {
+                const uint32_t cpr = p.tile_n / 8, col = n0 + 8 * (q % cpr);
+                if (col + 8 <= p.N) o = (k0 + q / cpr) * p.ldb * 2 + col * 2;   // whole chunks inside the row
+            }
+        }
+        off[j] = o;
+    }
+#pragma unroll 1
+    for (uint32_t s = 0; s < steps; s++) {
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const uint32_t w0 = j * 256 + wave * 64;            // the wave's first chunk: wave-uniform tests
+            if (w0 < cs) {
+                LDS_AS uint8_t* dst = (LDS_AS uint8_t*)lds + ((j & 3) * 4 + wave) * 1024;
+                if (w0 < ca)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void*)dst, 16,
+                                                            off[j] == t0::OOB_OFFSET ? off[j] : off[j] + s * 128, 0, 0, 0);
+                else
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void*)dst, 16,
+                                                            off[j] == t0::OOB_OFFSET ? off[j] : off[j] + s * adv_b, 0, 0, 0);
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
 // MFMA-issue floor of the 8-wave 256 x 256 GEMM: 512 threads per workgroup,
 // every wave loads two sets of operand fragments (4 A + 2 B, 16 bytes per
 // lane each, from src at (workgroup * 512 + thread) * 192 bytes) and issues

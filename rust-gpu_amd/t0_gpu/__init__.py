@@ -474,6 +474,12 @@ class GpuRuntime:
     def floor_stream_read(self, src, nbytes, sink, workgroups=256, threads=1024):
         _check(lib().t0_floor_stream_read(self.h, src, nbytes, sink, workgroups, threads))
 
+    def floor_tile_read(self, a, b, m, n, k, transpose=NT, mode=3, cfg: GemmConfig | None = None, lda=0, ldb=0):
+        """Only the operand slices of the GEMM tiling cfg (None: the pick) move
+        to LDS: mode 1 the A slices, 2 the B slices, 3 both.  Asynchronous."""
+        d = GemmDescC(a=a, b=b, m=m, n=n, k=k, lda=lda, ldb=ldb, transpose=transpose)
+        _check(lib().t0_floor_tile_read(self.h, C.byref(cfg) if cfg is not None else None, C.byref(d), mode))
+
     def floor_empty(self, workgroups=256, threads=1024):
         _check(lib().t0_floor_empty(self.h, workgroups, threads))
 

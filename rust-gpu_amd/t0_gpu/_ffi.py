@@ -153,6 +153,7 @@ SIGNATURES = {
     "t0_unpad_2d": ([vp, u64, u64, u32, u32, u32], C.c_int),
     "t0_copy_device": ([vp, u64, u64, u64], C.c_int),
     "t0_floor_stream_read": ([vp, u64, u64, u64, u32, u32], C.c_int),
+    "t0_floor_tile_read": ([vp, P(GemmConfigC), P(GemmDescC), C.c_int], C.c_int),
     "t0_floor_empty": ([vp, u32, u32], C.c_int),
     "t0_floor_mfma": ([vp, u64, u64, u32, u32], C.c_int),
     "t0_floor_lds": ([vp, C.c_int, u64, u64, u32, u32, u32], C.c_int),
