@@ -187,6 +187,34 @@ def bench_ceilings(rt, steps, warmup, rng):
     for b in ops + [rec, src64]:
         b.free()
     out["gemm_4096_zero_operands"] = bench_gemm_zero_operands(rt, steps, warmup)
+    out["w4a16_prefill_zero_activations"] = bench_prefill_zero_activations(rt, steps, warmup, rng)
+    return out
+
+
+def bench_prefill_zero_activations(rt, steps, warmup, rng):
+    """Not a BASELINE workload: the W4A16 prefill (4096x4096x14336, the
+    BASELINE weights, scales and zero points) timed with N(0,1) activations
+    and, on the same weights and kernel, with all-zero activations.  Only the
+    MFMAs' operand values differ, so the gap is what their data-dependent
+    power costs the prefill."""
+    m, n, k, gs = 4096, 14336, 4096, 128
+    qw, s, zw = _w4_operands(rng, n, k, gs, True)
+    dq, ds, dz = rt.upload(qw), rt.upload(s), rt.upload(zw)
+    dc = rt.alloc(m * n * 2)
+    a_n = rt.upload(bf16_rne(rng.standard_normal((m, k), dtype=np.float32)))
+    a_z = rt.alloc(m * k * 2)
+    rt.memset(a_z.gpu_addr(), 0, m * k * 2)
+    out = {}
+    for name, a in (("normal", a_n), ("zeros", a_z)):
+        def step():
+            rt.w4a16(a.gpu_addr(), dq.gpu_addr(), ds.gpu_addr(), dz.gpu_addr(), dc.gpu_addr(), m, n, k,
+                     group_size=gs, zero_const=0)
+        ms = Timer(rt).run(step, max(5, steps // 4), max(2, warmup // 2))
+        tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+        out[name] = {"us_per_launch": round(ms * 1e3, 1), "tflops": round(tflops, 1),
+                     "frac_of_peak": round(tflops / PEAK_TFLOPS, 4)}
+    for buf in (dq, ds, dz, dc, a_n, a_z):
+        buf.free()
     return out
 
 
