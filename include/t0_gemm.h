@@ -453,7 +453,8 @@ int t0_floor_empty(t0_runtime* rt, uint32_t workgroups, uint32_t threads);
  * LDS, 64 k per step, as the GEMM stages them: no MFMAs, no partial sums, no
  * stores.  The time the tiling's operand traffic takes on its own.  Tiled
  * configs with tile_m, tile_n multiples of 8, tile_m + tile_n <= 512, K a
- * multiple of 64 * split_k, operands under 4 GiB.  Asynchronous. */
+ * multiple of 64 * split_k, 16-byte aligned operands under 4 GiB with lda
+ * and ldb multiples of 8.  Asynchronous. */
 int t0_floor_tile_read(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm_desc* d, int mode);
 /* Ceilings of the compute-bound GEMM (measurement aids, no reference
  * counterpart).  t0_floor_mfma issues mfma_per_wave (a multiple of 16)

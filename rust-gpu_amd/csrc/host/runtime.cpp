@@ -1720,6 +1720,8 @@ int t0_floor_tile_read(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm_
     const bool nt = d->transpose == T0_NT;
     const uint64_t lda = d->lda ? d->lda : d->k, ldb = d->ldb ? d->ldb : (nt ? d->k : d->n);
     if (lda < d->k || ldb < (nt ? d->k : d->n)) return fail(T0_ERR_INVALID, "leading dimension below the row length");
+    if (!aligned16(d->a) || !aligned16(d->b) || lda % 8 || ldb % 8)
+        return fail(T0_ERR_INVALID, "16-byte aligned operands with lda %% 8 == 0 and ldb %% 8 == 0");
     if ((uint64_t)d->m * lda * 2 >= (1ull << 32) || (uint64_t)(nt ? d->n : d->k) * ldb * 2 >= (1ull << 32))
         return fail(T0_ERR_INVALID, "operands must stay under 4 GiB");
     const uint64_t tiles = (uint64_t)((d->m + c.tile_m - 1) / c.tile_m) * ((d->n + c.tile_n - 1) / c.tile_n);

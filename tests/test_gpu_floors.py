@@ -52,6 +52,10 @@ def test_floor_tile_read_refuses(rt, dev):
             rt.floor_tile_read(da, db, m, n, k, transpose=t0.NN, **kw)
     with pytest.raises(t0.T0Error):
         rt.floor_tile_read(da, db, m, n, k, transpose=t0.NN, mode=3, lda=k - 8)
+    with pytest.raises(t0.T0Error):
+        rt.floor_tile_read(da + 8, db, m, n, k, transpose=t0.NN, mode=3)          # misaligned A
+    with pytest.raises(t0.T0Error):
+        rt.floor_tile_read(da, db, m, n, k, transpose=t0.NN, mode=3, ldb=n + 4)   # ldb % 8 != 0
     # the runtime still computes: a small integer GEMM is exact
     rng = np.random.default_rng(7)
     a = rng.integers(-3, 4, (64, 256)).astype(np.float32)
