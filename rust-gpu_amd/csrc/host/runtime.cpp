@@ -205,7 +205,13 @@ int run_gemm_params(t0_runtime* rt, const GemmInstance* g, bool nn, t0_gemm_para
         const uint32_t tiles = ((p.M + 63) / 64) * ((p.N + 63) / 64) * p.split_k;
         return launch(rt, f, tiles, 1, 1, 256, p);
     }
-    int r = get_fn(rt, g->symbol(nn), &f);
+    std::string sym = g->symbol(nn);
+    // the register-staged variant of the skinny tile when every split-K
+    // partition is a whole number of pairs of 64-k steps (bit-identical)
+    if (g->bm == 64 && g->bn == 128 && g->bk == 64 && g->nw() == 4 && g->stages == 4 && p.split_k &&
+        p.K % (128u * p.split_k) == 0)
+        sym.insert(sym.size() - 3, "_vg2");
+    int r = get_fn(rt, sym, &f);
     if (r) return r;
     const uint32_t tiles = ((p.M + g->bm - 1) / g->bm) * ((p.N + g->bn - 1) / g->bn);
     if ((p.flags & T0_GEMM_FIXUP) && sc) {

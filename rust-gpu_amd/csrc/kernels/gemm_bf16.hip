@@ -150,7 +150,7 @@ T0_DEV void emit_rowblock(const t0_gemm_params& p, uint8_t* Cb, const float* wre
     }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool NN, int STAGES>
+template <int BM, int BN, int BK, int WM, int WN, bool NN, int STAGES, int VGD = 0>
 __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
     using G = GemmCfg<BM, BN, BK, WM, WN, NN, STAGES>;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[G::SMEM_BYTES];
@@ -588,7 +588,111 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
         }
     }
 
-    if constexpr (!PP) { if (!lean) {
+    // ---- register-staged K loop (VGD > 0; whole 64-k steps) -----------------
+    // For the memory-bound small tiles: every lane loads its 16-byte chunks of
+    // a stage into registers, VGD stages ahead, and writes them with
+    // ds_write_b128 to the position its global->LDS DMA would have filled
+    // (same swizzle, so the fragment reads are unchanged), into one of two
+    // LDS buffers.  Step t computes from buffer t % 2; in its first sub-step
+    // every wave writes stage t + 1 (its loads issued VGD - 1 steps earlier)
+    // to the other buffer, which step t - 1's barrier freed, and refills
+    // those registers with stage t + 1 + VGD; one barrier (LDS writes
+    // complete, no load wait) at the last sub-step.  The same MFMAs in the
+    // same order as the DMA loop: bit-identical.  On the skinny GEMM
+    // (128x4096x4096, 64x128 split 4) VGD = 2 takes 16.8-16.9 us against
+    // 17.3-17.4 by DMA (VGD 1: 19.0, 4: 17.2, 8: 17.2); a stage-read floor
+    // of that tiling moves its operand slices 13 % faster this way.
+    bool vg = false;
+    if constexpr (VGD > 0) vg = k_len % BK == 0 && nk % VGD == 0 && nk >= VGD;
+    if constexpr (VGD > 0) {
+        static_assert(KK >= 2 && KK % 2 == 0 && !PP && !LEAN, "register staging: the two-buffer loop");
+        if (vg) {
+            u32x4_t rg[VGD][G::LOADS];
+            // stage t into register set S; a stage past the last reads zeros
+            // without touching memory.  Branch-free (the offset is raised to
+            // OOB_OFFSET by a max with an opaque scalar), so every step issues
+            // the same loads and the compiler's load counting stays exact.
+            auto vg_issue = [&](auto Sc, uint32_t t) {
+                constexpr int S = decltype(Sc)::value;
+                const bool live = t < nk;
+                uint32_t lim = live ? 0u : OOB_OFFSET;
+                asm volatile("" : "+s"(lim));
+                const uint32_t kt = live ? t * BK : 0;
+                const __amdgpu_buffer_rsrc_t ra = make_rsrc(A0 + (size_t)kt * 2);
+                const __amdgpu_buffer_rsrc_t rb = make_rsrc(NN ? B0 + (size_t)kt * ldb * 2 : B0 + (size_t)kt * 2);
+#pragma unroll
+                for (int j = 0; j < G::A_LOADS; j++)
+                    rg[S][j] = buffer_load_x4(ra, ld.a_off[j] > lim ? ld.a_off[j] : lim);
+#pragma unroll
+                for (int j = 0; j < G::B_LOADS; j++)
+                    rg[S][G::A_LOADS + j] = buffer_load_x4(rb, ld.b_off[j] > lim ? ld.b_off[j] : lim);
+            };
+            auto vg_write = [&](auto Sc, uint32_t t) {
+                constexpr int S = decltype(Sc)::value;
+                LDS_AS uint8_t* st = (LDS_AS uint8_t*)smem + (t & 1) * G::STAGE_BYTES;
+#pragma unroll
+                for (int j = 0; j < G::A_LOADS; j++)
+                    *(LDS_AS u32x4_t*)(st + (wave * G::A_LOADS + j) * 1024 + lane * 16) = rg[S][j];
+#pragma unroll
+                for (int j = 0; j < G::B_LOADS; j++)
+                    *(LDS_AS u32x4_t*)(st + G::A_BYTES + (wave * G::B_LOADS + j) * 1024 + lane * 16) =
+                        rg[S][G::A_LOADS + j];
+            };
+            // LDS writes complete, then every wave at the barrier; loads stay in flight
+            auto vg_barrier = [&]() {
+                __builtin_amdgcn_sched_barrier(0);
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_sched_barrier(0);
+            };
+            auto buf = [&](uint32_t t) { return (const LDS_AS uint8_t*)smem + (t & 1) * G::STAGE_BYTES; };
+            static_for<0, VGD>([&](auto U) { vg_issue(U, decltype(U)::value); });
+            y_split_stride = p.y_split_stride;
+            asm volatile("" : "+s"(y_split_stride));
+            vg_write(Idx<0>{}, 0);
+            vg_issue(Idx<0>{}, VGD);
+            vg_barrier();
+            bf16x8_t af[2][G::FM], bfr[2][G::FN];
+            load_frags(buf(0), 0, af[0], bfr[0]);
+            // step t; NS = the register set of stage t + 1; MORE = t + 1 < nk
+            auto vg_step = [&](uint32_t t, auto NSc, auto MOREc) {
+                constexpr bool MORE = decltype(MOREc)::value != 0;
+                const LDS_AS uint8_t* sa = buf(t);
+#pragma unroll
+                for (int kk = 0; kk < KK; kk++) {
+                    const int cur = kk & 1;
+                    if (kk + 1 < KK) {
+                        load_frags(sa, kk + 1, af[cur ^ 1], bfr[cur ^ 1]);
+                    } else if constexpr (MORE) {
+                        vg_barrier();
+                        load_frags(buf(t + 1), 0, af[cur ^ 1], bfr[cur ^ 1]);
+                    }
+                    mfmas(af[cur], bfr[cur]);
+                    if constexpr (MORE) {
+                        if (kk == 0) {
+                            vg_write(NSc, t + 1);
+                            vg_issue(NSc, t + 1 + VGD);
+                        }
+                    }
+                    order_substep();
+                }
+            };
+            // whole groups of VGD steps (nk % VGD == 0), the last one peeled
+            uint32_t t0 = 0;
+            for (; t0 + VGD < nk; t0 += VGD)
+                static_for<0, VGD>([&](auto U) {
+                    constexpr int u = decltype(U)::value;
+                    vg_step(t0 + u, Idx<(u + 1) % VGD>{}, Idx<1>{});
+                });
+            static_for<0, VGD>([&](auto U) {
+                constexpr int u = decltype(U)::value;
+                vg_step(t0 + u, Idx<(u + 1) % VGD>{}, Idx<(u + 1 < VGD ? 1 : 0)>{});
+            });
+        }
+    }
+
+    if constexpr (!PP) { if (!lean && !vg) {
     // prologue: every buffer, then stage 0 visible and its first fragments
 #pragma unroll
     for (int s = 0; s < STAGES; s++)
@@ -660,7 +764,7 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
             }
         }
     }
-    } }   // !PP, !lean
+    } }   // !PP, !lean, !vg
 
     // ---- epilogue -----------------------------------------------------------
     // acc[i][j][r] holds C[m0 + wm*TM + i*32 + lane%32][n0 + wn*TN + j*32 + 8*(r/4) + 4*(lane/32) + r%4].
@@ -765,6 +869,18 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
     T0_GEMM_INSTANCE(BM, BN, BK, WM, WN, ST, false, nt) \
     T0_GEMM_INSTANCE(BM, BN, BK, WM, WN, ST, true, nn)
 
+// Register-staged variants (suffix _vg<D>): the same tile with the K loop
+// staged through registers D stages ahead; the host takes them when every
+// split-K partition is a whole number of D 64-k steps.
+#define T0_GEMM_VG_INSTANCE(BM, BN, BK, WM, WN, ST, D, NNF, TAG)                                    \
+    extern "C" __global__ void __launch_bounds__(WM * WN * 64)                                      \
+        t0k_gemm_##BM##x##BN##x##BK##_w##WM##x##WN##_s##ST##_vg##D##_##TAG(const t0_gemm_params p) { \
+        t0::gemm_tile_kernel<BM, BN, BK, WM, WN, NNF, ST, D>(p);                                    \
+    }
+#define T0_GEMM_VG_BOTH(BM, BN, BK, WM, WN, ST, D)             \
+    T0_GEMM_VG_INSTANCE(BM, BN, BK, WM, WN, ST, D, false, nt) \
+    T0_GEMM_VG_INSTANCE(BM, BN, BK, WM, WN, ST, D, true, nn)
+
 // gfx950-native tiles (auto-selection targets); stages = LDS buffers in flight
 T0_GEMM_BOTH(256, 256, 64, 2, 2, 2)
 T0_GEMM_BOTH(256, 256, 64, 2, 4, 2)
@@ -777,6 +893,7 @@ T0_GEMM_BOTH(128, 128, 64, 2, 2, 4)
 T0_GEMM_BOTH(128, 128, 32, 2, 2, 4)
 T0_GEMM_BOTH(128, 64, 64, 2, 2, 4)
 T0_GEMM_BOTH(64, 128, 64, 2, 2, 4)
+T0_GEMM_VG_BOTH(64, 128, 64, 2, 2, 4, 2)
 T0_GEMM_BOTH(64, 64, 64, 2, 2, 4)
 T0_GEMM_BOTH(64, 64, 64, 1, 1, 4)
 T0_GEMM_BOTH(32, 64, 64, 1, 1, 6)

@@ -195,6 +195,31 @@ def test_eight_wave_256_tiles(rt, dev, m, n, k):
             assert np.array_equal(got16, f32(orc.bf16_rne(want.astype(np.float32)))), (cfg.name(), m, n, k, layout)
 
 
+@pytest.mark.parametrize("m,n,k,sk", [(128, 512, 1024, 1), (128, 512, 1024, 4), (100, 520, 1024, 2),
+                                      (128, 4096, 4096, 4), (64, 256, 256, 2), (64, 256, 128, 2), (128, 512, 1000, 1),
+                                      (130, 384, 1536, 8)])
+def test_register_staged_64x128_tile(rt, dev, m, n, k, sk):
+    """The 64x128x64 four-wave tile, whose K loop is staged through registers
+    when every split-K partition is a whole number of pairs of 64-k steps
+    (K % (128 * split) == 0; else the DMA loop runs): one and many pairs per
+    partition, ragged M / N, the skinny shape, partitions of one step and a
+    K tail (DMA loop), NN and NT, f32 and bf16 out, in-kernel split-K.
+    Small-integer operands keep every partial sum exact."""
+    print(f"register-staged 64x128: m={m} n={n} k={k} split={sk}", flush=True)
+    rng = np.random.default_rng(m * 7 + n + k + sk)
+    ai = rng.integers(-8, 9, size=(m, k))
+    bi = rng.integers(-6, 7, size=(k, n))
+    want = ai.astype(np.int64) @ bi.astype(np.int64)
+    a, b = bf16(ai), bf16(bi)
+    cfg = t0.GemmConfig.tile_64x128_k64().copy(wg_size=256, split_k=sk if sk > 1 else 0)
+    for layout, bb in ((t0.NN, b), (t0.NT, bf16(bi.T.copy()))):
+        got = run_gemm(rt, dev, a, bb, m, n, k, layout, t0.OUT_F32, cfg=cfg.copy(transpose=layout))
+        assert np.array_equal(got.astype(np.int64), want), (cfg.name(), m, n, k, sk, layout)
+        got16 = run_gemm(rt, dev, a, bb, m, n, k, layout, t0.OUT_BF16,
+                         cfg=cfg.copy(transpose=layout, out_dtype=t0.OUT_BF16))
+        assert np.array_equal(got16, f32(orc.bf16_rne(want.astype(np.float32)))), (cfg.name(), m, n, k, sk, layout)
+
+
 @pytest.mark.parametrize("sk", [1, 2, 4])
 def test_eight_wave_256x64_split_k_and_bias(rt, dev, sk):
     """The 8-wave 256x256x64 instance on interior tiles with whole 64-k steps
