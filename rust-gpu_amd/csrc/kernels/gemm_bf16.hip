@@ -821,7 +821,9 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
     if (!publish_and_count(&p.semaphores[tile_id], sk, &s_last)) return;
     // The lane's NOUT 16-byte outputs are summed over the planes in plane
     // order; the loads of up to 32 (output, plane) pairs go out before any is
-    // consumed (planes past split_k are not loaded).
+    // consumed (planes past split_k are not loaded).  With few outputs per
+    // lane (registers to spare) this partition's own plane comes from its
+    // registers, the values it stored, instead of being reloaded.
     constexpr int NJ = G::FN * 4, NOUT = G::FM * NJ;
     constexpr int QB = NOUT >= 32 ? 1 : 32 / NOUT;   // planes per batch
     f32x4_t v[NOUT];
@@ -833,6 +835,14 @@ __device__ __forceinline__ void gemm_tile_kernel(const t0_gemm_params& p) {
 #pragma unroll
         for (int qq = 0; qq < QB; qq++) {
             if (q0 + qq >= sk) break;                    // uniform
+            if (NOUT <= 8 && q0 + qq == part) {          // uniform
+#pragma unroll
+                for (int o = 0; o < NOUT; o++) {
+                    const int i = o / NJ, j = (o % NJ) / 4, g = o % 4;
+                    t[o][qq] = f32x4_t{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+                }
+                continue;
+            }
 #pragma unroll
             for (int o = 0; o < NOUT; o++)
                 t[o][qq] = ld_agent_x4(rws, ((uint32_t)o * G::NT + tid) * 16 + (q0 + qq) * TILE_BYTES);
