@@ -193,6 +193,17 @@ struct Scratch {
     size_t bytes = 0;
 };
 
+// The register-staged K loop (t0k_gemm_*_vg2_*) where it measured faster
+// than the DMA loop (graph replays, B cold, the pick on each shape): the
+// 64x128 four-wave tile (128x4096x4096 0.97x) and the 128x64 one with no
+// fully masked rows (M 128-512: 0.93-1.00x; at M = 32 it lost 7 %).  The
+// 128x128, 64x64 and 32-row tiles lost 2-13 % and keep the DMA loop.
+bool use_vg_variant(const GemmInstance& g, const t0_gemm_params& p) {
+    if (g.bk != 64 || g.wm != 2 || g.wn != 2 || g.stages != 4) return false;
+    if (g.bm == 64 && g.bn == 128) return true;
+    return g.bm == 128 && g.bn == 64 && p.M >= 128;
+}
+
 int run_gemm_params(t0_runtime* rt, const GemmInstance* g, bool nn, t0_gemm_params& p, uint32_t threads_override = 0,
                     bool b_cols_padded = false, const Scratch* sc = nullptr) {
     hipFunction_t f;
@@ -206,10 +217,9 @@ int run_gemm_params(t0_runtime* rt, const GemmInstance* g, bool nn, t0_gemm_para
         return launch(rt, f, tiles, 1, 1, 256, p);
     }
     std::string sym = g->symbol(nn);
-    // the register-staged variant of the skinny tile when every split-K
-    // partition is a whole number of pairs of 64-k steps (bit-identical)
-    if (g->bm == 64 && g->bn == 128 && g->bk == 64 && g->nw() == 4 && g->stages == 4 && p.split_k &&
-        p.K % (128u * p.split_k) == 0)
+    // the register-staged variant when every split-K partition is a whole
+    // number of pairs of 64-k steps (bit-identical)
+    if (use_vg_variant(*g, p) && p.split_k && p.K % (128u * p.split_k) == 0)
         sym.insert(sym.size() - 3, "_vg2");
     int r = get_fn(rt, sym, &f);
     if (r) return r;

@@ -904,6 +904,7 @@ T0_GEMM_BOTH(128, 128, 32, 2, 2, 4)
 T0_GEMM_BOTH(128, 64, 64, 2, 2, 4)
 T0_GEMM_BOTH(64, 128, 64, 2, 2, 4)
 T0_GEMM_VG_BOTH(64, 128, 64, 2, 2, 4, 2)
+T0_GEMM_VG_BOTH(128, 64, 64, 2, 2, 4, 2)
 T0_GEMM_BOTH(64, 64, 64, 2, 2, 4)
 T0_GEMM_BOTH(64, 64, 64, 1, 1, 4)
 T0_GEMM_BOTH(32, 64, 64, 1, 1, 6)

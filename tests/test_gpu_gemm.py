@@ -198,20 +198,23 @@ def test_eight_wave_256_tiles(rt, dev, m, n, k):
 @pytest.mark.parametrize("m,n,k,sk", [(128, 512, 1024, 1), (128, 512, 1024, 4), (100, 520, 1024, 2),
                                       (128, 4096, 4096, 4), (64, 256, 256, 2), (64, 256, 128, 2), (128, 512, 1000, 1),
                                       (130, 384, 1536, 8)])
-def test_register_staged_64x128_tile(rt, dev, m, n, k, sk):
-    """The 64x128x64 four-wave tile, whose K loop is staged through registers
-    when every split-K partition is a whole number of pairs of 64-k steps
-    (K % (128 * split) == 0; else the DMA loop runs): one and many pairs per
-    partition, ragged M / N, the skinny shape, partitions of one step and a
-    K tail (DMA loop), NN and NT, f32 and bf16 out, in-kernel split-K.
-    Small-integer operands keep every partial sum exact."""
-    print(f"register-staged 64x128: m={m} n={n} k={k} split={sk}", flush=True)
+@pytest.mark.parametrize("tile", ["64x128", "128x64"])
+def test_register_staged_tiles(rt, dev, m, n, k, sk, tile):
+    """The 64x128x64 and 128x64x64 four-wave tiles, whose K loop is staged
+    through registers when every split-K partition is a whole number of
+    pairs of 64-k steps (K % (128 * split) == 0; for 128x64 also M >= 128;
+    else the DMA loop runs): one and many pairs per partition, ragged M / N,
+    the skinny shape, partitions of one step and a K tail (DMA loop), NN and
+    NT, f32 and bf16 out, in-kernel split-K.  Small-integer operands keep
+    every partial sum exact."""
+    print(f"register-staged {tile}: m={m} n={n} k={k} split={sk}", flush=True)
     rng = np.random.default_rng(m * 7 + n + k + sk)
     ai = rng.integers(-8, 9, size=(m, k))
     bi = rng.integers(-6, 7, size=(k, n))
     want = ai.astype(np.int64) @ bi.astype(np.int64)
     a, b = bf16(ai), bf16(bi)
-    cfg = t0.GemmConfig.tile_64x128_k64().copy(wg_size=256, split_k=sk if sk > 1 else 0)
+    base = t0.GemmConfig.tile_64x128_k64() if tile == "64x128" else t0.GemmConfig.tile_128x64_k64()
+    cfg = base.copy(wg_size=256, split_k=sk if sk > 1 else 0)
     for layout, bb in ((t0.NN, b), (t0.NT, bf16(bi.T.copy()))):
         got = run_gemm(rt, dev, a, bb, m, n, k, layout, t0.OUT_F32, cfg=cfg.copy(transpose=layout))
         assert np.array_equal(got.astype(np.int64), want), (cfg.name(), m, n, k, sk, layout)
