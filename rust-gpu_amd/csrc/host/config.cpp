@@ -167,25 +167,22 @@ static uint32_t est_vgprs(const GemmInstance& g) {
 //                  re-reads (A once per column tile, B once per row tile)
 //                  over L2_TBS;
 //   split-K        + FIX us + FIX_MB us per MB of partial tiles.
-// Least squares on log time, refined for the picks (the measured regret of
-// a soft minimum over the predicted times, plus 3 x the squared log error):
-// median error 16 %; on the fitted data the pick is within 3 % of the
-// measured best on 24 of the 28 shapes (22 with each shape left out of the
-// fit), and the measured best is among the 4 best-predicted candidates on
-// every shape, so the tuner's candidates (t0_tune, top 8) always include it.
-// Re-measured on another box: the pick within 3 % on 19 of 28, at most
-// 22 % slower (the candidates' times move by up to ~15 % box to box).
+// Least squares on log time: median error 9 %; the pick is within 3 % of
+// the measured best on 16 of the 28 shapes (also with each shape left out
+// of the fit), at most 27.5 % slower (32 x 11008 x 4096), and the measured
+// best is among the 4 best-predicted candidates on every shape, so the
+// tuner's candidates (t0_tune, top 8) always include it.
 struct TileCost {
     uint32_t bm, bn, bk, nw;
     double a_us, b_us;
 };
 constexpr TileCost kTileCost[] = {
-    {256, 256, 64, 8, 21.56, 15.95}, {256, 128, 64, 4, 13.50, 18.01}, {128, 256, 64, 4, 19.64, 14.25},
-    {128, 128, 64, 4, 11.29, 7.63},  {128, 64, 64, 4, 2.79, 9.67},    {64, 128, 64, 4, 5.36, 7.79},
-    {64, 64, 64, 1, 4.97, 8.34},     {32, 128, 64, 2, 9.72, 7.10},    {32, 64, 64, 1, 3.07, 5.79},
+    {256, 256, 64, 8, 21.31, 17.22}, {256, 128, 64, 4, 11.93, 12.65}, {128, 256, 64, 4, 12.84, 13.10},
+    {128, 128, 64, 4, 7.84, 7.50},   {128, 64, 64, 4, 5.16, 5.32},    {64, 128, 64, 4, 4.91, 5.52},
+    {64, 64, 64, 1, 4.37, 6.47},     {32, 128, 64, 2, 8.45, 6.25},    {32, 64, 64, 1, 3.19, 5.43},
 };
-constexpr double kDisc = 1.000, kFixUs = 0.000, kFixUsPerMB = 0.369;
-constexpr double kHbmTBs = 3.757, kL2TBs = 13.539, kCoResident = 0.619;
+constexpr double kDisc = 0.964, kFixUs = 1.430, kFixUsPerMB = 0.462;
+constexpr double kHbmTBs = 3.678, kL2TBs = 14.734, kCoResident = 0.517;
 
 std::vector<Candidate> rank_candidates(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype,
                                        bool allow_fixup) {

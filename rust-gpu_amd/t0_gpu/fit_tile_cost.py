@@ -11,19 +11,15 @@ resident, a partly filled last round costing DISC + (1 - DISC) * fill of a
 round; co-resident workgroups at most 1 / CO as fast each; no faster than
 A + B + C over HBM, nor the operand re-reads over L2; split-K adding FIX +
 FIX_MB per MB of partial tiles.  Least squares on log time from several
-starts, then a ranking refinement: per shape, the measured log regret of
-the candidates weighted by a soft minimum of the predicted times (what the
-pick costs), plus W_ERR x the mean squared log error (so the predicted
-times stay meaningful), minimised by Powell's method from the least-squares
-fit.  Prints the fitted constants, the pick's regret (pick / measured best)
-per shape, and the same with each shape left out of the fit."""
+starts; prints the fitted constants, the pick's regret (pick / measured
+best) per shape, and the same with each shape left out of the fit."""
 import json
 import math
 import re
 import sys
 
 import numpy as np
-from scipy.optimize import least_squares, minimize
+from scipy.optimize import least_squares
 
 CUS, LDS = 256.0, 160 * 1024.0
 NAME = re.compile(r"t0_gemm_(\d+)x(\d+)_k(\d+)_ldsdb(?:_sk(\d+))?_nn_bf16 w(\d+)")
@@ -118,7 +114,8 @@ def fit(data, starts=8, seed=0):
     def resid(p):
         return np.log(np.maximum(predict_all(p, A), 1e-3) / A["meas"])
 
-    lo, hi = LO, HI
+    lo = [0.1, 0.1] * len(TILES) + [0.5, 0.0, 0.0, 1.0, 2.0, 0.2]
+    hi = [60.0, 60.0] * len(TILES) + [1.0, 20.0, 5.0, 8.0, 40.0, 1.0]
     best = None
     for _ in range(starts):
         x0 = [rng.uniform(l, h) for l, h in zip(lo, hi)]
@@ -126,34 +123,6 @@ def fit(data, starts=8, seed=0):
         if best is None or r.cost < best.cost:
             best = r
     return best.x, float(np.median(np.abs(np.exp(best.fun) - 1)))
-
-
-W_ERR, TAU = 3.0, 0.05
-LO = [0.1, 0.1] * len(TILES) + [0.5, 0.0, 0.0, 1.0, 2.0, 0.2]
-HI = [60.0, 60.0] * len(TILES) + [1.0, 20.0, 5.0, 8.0, 40.0, 1.0]
-
-
-def fit_rank(data, p0):
-    """The least-squares fit p0 refined for the picks (see the module doc)."""
-    shapes = []
-    for shape, cands in data:
-        A = _arrays([(shape, cands)])
-        shapes.append((A, np.log(A["meas"] / A["meas"].min())))
-    A_all = _arrays(data)
-    lo, hi = np.array(LO), np.array(HI)
-
-    def obj(x):
-        p = np.clip(x, lo, hi)
-        tot = 0.0
-        for A, lr in shapes:
-            pr = np.log(np.maximum(predict_all(p, A), 1e-3))
-            w = np.exp(-(pr - pr.min()) / TAU)
-            tot += float((w * lr).sum() / w.sum())
-        err = np.log(np.maximum(predict_all(p, A_all), 1e-3) / A_all["meas"])
-        return tot + W_ERR * float(np.mean(err ** 2))
-
-    r = minimize(obj, p0, method="Powell", options={"maxiter": 20000, "xtol": 1e-3, "ftol": 1e-6})
-    return np.clip(r.x, lo, hi)
 
 
 def regrets(params, data):
@@ -167,9 +136,7 @@ def regrets(params, data):
 
 def main():
     data = load(sys.argv[1])
-    params = fit_rank(data, fit(data)[0])
-    A = _arrays(data)
-    med_err = float(np.median(np.abs(predict_all(params, A) / A["meas"] - 1)))
+    params, med_err = fit(data)
     reg = regrets(params, data)
     print(f"fit: median |pred/meas - 1| {med_err:.3f}; pick regret median {np.median(reg):.3f}, "
           f"max {max(reg):.3f}, within 3% on {sum(r <= 1.03 for r in reg)} of {len(reg)}")
@@ -180,8 +147,7 @@ def main():
     print(f"constexpr double kHbmTBs = {hbm:.3f}, kL2TBs = {l2:.3f}, kCoResident = {co:.3f};")
     loo = []
     for j in range(len(data)):
-        sub = data[:j] + data[j + 1:]
-        p = fit_rank(sub, fit(sub, starts=3, seed=j + 1)[0])
+        p, _ = fit(data[:j] + data[j + 1:], starts=3, seed=j + 1)
         loo.append(regrets(p, [data[j]])[0])
     print(f"leave-one-shape-out regret: median {np.median(loo):.3f}, max {max(loo):.3f}, "
           f"within 3% on {sum(r <= 1.03 for r in loo)} of {len(loo)}")
