@@ -167,22 +167,26 @@ static uint32_t est_vgprs(const GemmInstance& g) {
 //                  re-reads (A once per column tile, B once per row tile)
 //                  over L2_TBS;
 //   split-K        + FIX us + FIX_MB us per MB of partial tiles.
-// Least squares on log time: median error 9 %; the pick is within 3 % of
-// the measured best on 16 of the 28 shapes (also with each shape left out
-// of the fit), at most 27.5 % slower (32 x 11008 x 4096), and the measured
-// best is among the 4 best-predicted candidates on every shape, so the
-// tuner's candidates (t0_tune, top 8) always include it.
+// Fitted to the geometric mean of three runs (the candidates' times move by
+// a median 1 %, up to ~15 % run to run): least squares on log time, then
+// refined for the picks (the measured regret under a soft minimum of the
+// predicted times, plus 3 x the squared log error); median error 17 %.
+// The pick is within 3 % of the measured best on 23 of the 28 shapes (21
+// with each shape left out of the fit; least squares alone: 18), at most
+// 18 % slower (32 x 11008 x 4096), and the measured best is among the 4
+// best-predicted candidates on every shape, so the tuner's candidates
+// (t0_tune, top 8) always include it.
 struct TileCost {
     uint32_t bm, bn, bk, nw;
     double a_us, b_us;
 };
 constexpr TileCost kTileCost[] = {
-    {256, 256, 64, 8, 21.31, 17.22}, {256, 128, 64, 4, 11.93, 12.65}, {128, 256, 64, 4, 12.84, 13.10},
-    {128, 128, 64, 4, 7.84, 7.50},   {128, 64, 64, 4, 5.16, 5.32},    {64, 128, 64, 4, 4.91, 5.52},
-    {64, 64, 64, 1, 4.37, 6.47},     {32, 128, 64, 2, 8.45, 6.25},    {32, 64, 64, 1, 3.19, 5.43},
+    {256, 256, 64, 8, 0.10, 20.73}, {256, 128, 64, 4, 8.77, 13.09}, {128, 256, 64, 4, 7.37, 18.08},
+    {128, 128, 64, 4, 1.73, 11.33}, {128, 64, 64, 4, 0.10, 11.21},  {64, 128, 64, 4, 0.20, 9.81},
+    {64, 64, 64, 1, 1.62, 10.45},   {32, 128, 64, 2, 5.34, 9.28},   {32, 64, 64, 1, 2.42, 6.46},
 };
-constexpr double kDisc = 0.964, kFixUs = 1.430, kFixUsPerMB = 0.462;
-constexpr double kHbmTBs = 3.678, kL2TBs = 14.734, kCoResident = 0.517;
+constexpr double kDisc = 1.000, kFixUs = 0.000, kFixUsPerMB = 0.704;
+constexpr double kHbmTBs = 3.744, kL2TBs = 12.081, kCoResident = 0.580;
 
 std::vector<Candidate> rank_candidates(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype,
                                        bool allow_fixup) {

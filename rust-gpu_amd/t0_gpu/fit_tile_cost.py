@@ -3,7 +3,9 @@ kTileCost and the constants beside it) to the measurements that
 ``python bench.py --only tiles`` prints: every ranked tile x split-K
 candidate timed on LLM shapes (NN, bf16 out, weight operand read cold).
 
-    python rust-gpu_amd/t0_gpu/fit_tile_cost.py tiles.json
+    python rust-gpu_amd/t0_gpu/fit_tile_cost.py tiles.json [tiles2.json ...]
+
+Several runs are averaged per candidate (geometric mean of the times).
 
 The model is the one rank_candidates evaluates: per workgroup a + b * k_len
 / 1000 us while a round of workgroups (CUs x workgroups per CU, by LDS) is
@@ -11,15 +13,19 @@ resident, a partly filled last round costing DISC + (1 - DISC) * fill of a
 round; co-resident workgroups at most 1 / CO as fast each; no faster than
 A + B + C over HBM, nor the operand re-reads over L2; split-K adding FIX +
 FIX_MB per MB of partial tiles.  Least squares on log time from several
-starts; prints the fitted constants, the pick's regret (pick / measured
-best) per shape, and the same with each shape left out of the fit."""
+starts, then a ranking refinement: per shape, the measured log regret of
+the candidates weighted by a soft minimum of the predicted times (what the
+pick costs), plus W_ERR x the mean squared log error (so the predicted
+times stay meaningful), minimised by Powell's method from the least-squares
+fit.  Prints the fitted constants, the pick's regret (pick / measured best)
+per shape, and the same with each shape left out of the fit."""
 import json
 import math
 import re
 import sys
 
 import numpy as np
-from scipy.optimize import least_squares
+from scipy.optimize import least_squares, minimize
 
 CUS, LDS = 256.0, 160 * 1024.0
 NAME = re.compile(r"t0_gemm_(\d+)x(\d+)_k(\d+)_ldsdb(?:_sk(\d+))?_nn_bf16 w(\d+)")
@@ -61,16 +67,30 @@ def predict(params, t, sk, m, n, k):
     return tm
 
 
-def load(path):
-    d = json.load(open(path))
+def _last_json(path):
+    with open(path) as f:
+        return json.loads(f.read().strip().splitlines()[-1])
+
+
+def load(*paths):
+    """Shapes and their candidates' times; with several runs, the geometric
+    mean of each candidate's times over the runs that timed it in all."""
+    runs = [_last_json(p) for p in paths]
     data = []
-    for r in d["shapes"]:
-        m, n, k = r["shape"]
+    for shapes in zip(*[r["shapes"] for r in runs]):
+        m, n, k = shapes[0]["shape"]
+        assert all(list(s["shape"]) == [m, n, k] for s in shapes), "runs over different shapes"
+        times = {}
+        for s in shapes:
+            for name, _est, meas in s["all"]:
+                times.setdefault(name, []).append(meas)
         cands = []
-        for name, _est, meas in r["all"]:
+        for name, ts in times.items():
+            if len(ts) != len(runs):
+                continue
             g = NAME.fullmatch(name)
             bm, bn, bk, sk, w = int(g[1]), int(g[2]), int(g[3]), int(g[4] or 1), int(g[5])
-            cands.append(((bm, bn, bk, w), sk, meas))
+            cands.append(((bm, bn, bk, w), sk, float(np.exp(np.mean(np.log(ts))))))
         data.append(((m, n, k), cands))
     return data
 
@@ -114,8 +134,7 @@ def fit(data, starts=8, seed=0):
     def resid(p):
         return np.log(np.maximum(predict_all(p, A), 1e-3) / A["meas"])
 
-    lo = [0.1, 0.1] * len(TILES) + [0.5, 0.0, 0.0, 1.0, 2.0, 0.2]
-    hi = [60.0, 60.0] * len(TILES) + [1.0, 20.0, 5.0, 8.0, 40.0, 1.0]
+    lo, hi = LO, HI
     best = None
     for _ in range(starts):
         x0 = [rng.uniform(l, h) for l, h in zip(lo, hi)]
@@ -123,6 +142,34 @@ def fit(data, starts=8, seed=0):
         if best is None or r.cost < best.cost:
             best = r
     return best.x, float(np.median(np.abs(np.exp(best.fun) - 1)))
+
+
+W_ERR, TAU = 3.0, 0.05
+LO = [0.1, 0.1] * len(TILES) + [0.5, 0.0, 0.0, 1.0, 2.0, 0.2]
+HI = [60.0, 60.0] * len(TILES) + [1.0, 20.0, 5.0, 8.0, 40.0, 1.0]
+
+
+def fit_rank(data, p0):
+    """The least-squares fit p0 refined for the picks (see the module doc)."""
+    shapes = []
+    for shape, cands in data:
+        A = _arrays([(shape, cands)])
+        shapes.append((A, np.log(A["meas"] / A["meas"].min())))
+    A_all = _arrays(data)
+    lo, hi = np.array(LO), np.array(HI)
+
+    def obj(x):
+        p = np.clip(x, lo, hi)
+        tot = 0.0
+        for A, lr in shapes:
+            pr = np.log(np.maximum(predict_all(p, A), 1e-3))
+            w = np.exp(-(pr - pr.min()) / TAU)
+            tot += float((w * lr).sum() / w.sum())
+        err = np.log(np.maximum(predict_all(p, A_all), 1e-3) / A_all["meas"])
+        return tot + W_ERR * float(np.mean(err ** 2))
+
+    r = minimize(obj, p0, method="Powell", options={"maxiter": 20000, "xtol": 1e-3, "ftol": 1e-6})
+    return np.clip(r.x, lo, hi)
 
 
 def regrets(params, data):
@@ -135,8 +182,10 @@ def regrets(params, data):
 
 
 def main():
-    data = load(sys.argv[1])
-    params, med_err = fit(data)
+    data = load(*sys.argv[1:])
+    params = fit_rank(data, fit(data)[0])
+    A = _arrays(data)
+    med_err = float(np.median(np.abs(predict_all(params, A) / A["meas"] - 1)))
     reg = regrets(params, data)
     print(f"fit: median |pred/meas - 1| {med_err:.3f}; pick regret median {np.median(reg):.3f}, "
           f"max {max(reg):.3f}, within 3% on {sum(r <= 1.03 for r in reg)} of {len(reg)}")
@@ -147,7 +196,8 @@ def main():
     print(f"constexpr double kHbmTBs = {hbm:.3f}, kL2TBs = {l2:.3f}, kCoResident = {co:.3f};")
     loo = []
     for j in range(len(data)):
-        p, _ = fit(data[:j] + data[j + 1:], starts=3, seed=j + 1)
+        sub = data[:j] + data[j + 1:]
+        p = fit_rank(sub, fit(sub, starts=3, seed=j + 1)[0])
         loo.append(regrets(p, [data[j]])[0])
     print(f"leave-one-shape-out regret: median {np.median(loo):.3f}, max {max(loo):.3f}, "
           f"within 3% on {sum(r <= 1.03 for r in loo)} of {len(loo)}")
