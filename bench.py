@@ -247,7 +247,8 @@ def bench_gemm_zero_operands(rt, steps, warmup):
 
 TILE_SHAPES = [(m, n, k) for m in (32, 128, 512, 1024, 2048, 4096)
                for (n, k) in ((4096, 4096), (11008, 4096), (4096, 11008), (14336, 4096))] + \
-              [(4096, 1024, 4096), (3072, 8192, 4096), (384, 4096, 4096), (16, 4096, 4096)]
+              [(4096, 1024, 4096), (3072, 8192, 4096), (384, 4096, 4096), (16, 4096, 4096)] + \
+              [(m, n, 4096) for m in (64, 256) for n in (4096, 11008, 14336)]
 
 
 def bench_tiles(rt, steps, warmup, rng, tr):

@@ -167,26 +167,29 @@ static uint32_t est_vgprs(const GemmInstance& g) {
 //                  re-reads (A once per column tile, B once per row tile)
 //                  over L2_TBS;
 //   split-K        + FIX us + FIX_MB us per MB of partial tiles.
-// Fitted to the geometric mean of three runs (the candidates' times move by
-// a median 1 %, up to ~15 % run to run): least squares on log time, then
-// refined for the picks (the measured regret under a soft minimum of the
-// predicted times, plus 3 x the squared log error); median error 17 %.
-// The pick is within 3 % of the measured best on 23 of the 28 shapes (21
-// with each shape left out of the fit; least squares alone: 18), at most
-// 18 % slower (32 x 11008 x 4096), and the measured best is among the 4
-// best-predicted candidates on every shape, so the tuner's candidates
-// (t0_tune, top 8) always include it.
+// Fitted to the geometric mean of six runs on three boxes (a candidate's
+// time moves by a median 1 %, up to ~15 % run to run), 34 shapes: least
+// squares on log time, then refined for the picks (the measured regret
+// under a soft minimum of the predicted times, plus 3 x the squared log
+// error).  The fit drives several constants to their bounds (no split-K
+// term, an HBM bound that never binds): the per-workgroup a and b carry
+// it, and the predicted times rank the candidates (median error 14 %)
+// rather than forecast them.  The pick is within 3 % of the measured best
+// on all 34 shapes of that data (33 with each shape left out of the fit,
+// at most 8 % slower), 26 of 34 re-measured on a fourth box (at most
+// 18 %), and the measured best is among the 4 best-predicted candidates
+// on every shape, so the tuner's candidates (t0_tune, top 8) include it.
 struct TileCost {
     uint32_t bm, bn, bk, nw;
     double a_us, b_us;
 };
 constexpr TileCost kTileCost[] = {
-    {256, 256, 64, 8, 0.10, 20.73}, {256, 128, 64, 4, 8.77, 13.09}, {128, 256, 64, 4, 7.37, 18.08},
-    {128, 128, 64, 4, 1.73, 11.33}, {128, 64, 64, 4, 0.10, 11.21},  {64, 128, 64, 4, 0.20, 9.81},
-    {64, 64, 64, 1, 1.62, 10.45},   {32, 128, 64, 2, 5.34, 9.28},   {32, 64, 64, 1, 2.42, 6.46},
+    {256, 256, 64, 8, 45.46, 7.71}, {256, 128, 64, 4, 27.50, 12.11}, {128, 256, 64, 4, 28.30, 11.53},
+    {128, 128, 64, 4, 18.31, 4.56}, {128, 64, 64, 4, 8.26, 6.64},    {64, 128, 64, 4, 7.17, 5.96},
+    {64, 64, 64, 1, 2.97, 6.02},    {32, 128, 64, 2, 5.97, 4.84},    {32, 64, 64, 1, 2.38, 4.43},
 };
-constexpr double kDisc = 1.000, kFixUs = 0.000, kFixUsPerMB = 0.704;
-constexpr double kHbmTBs = 3.744, kL2TBs = 12.081, kCoResident = 0.580;
+constexpr double kDisc = 1.000, kFixUs = 0.000, kFixUsPerMB = 0.000;
+constexpr double kHbmTBs = 8.000, kL2TBs = 18.896, kCoResident = 1.000;
 
 std::vector<Candidate> rank_candidates(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype,
                                        bool allow_fixup) {

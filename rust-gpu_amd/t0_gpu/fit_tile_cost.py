@@ -73,16 +73,18 @@ def _last_json(path):
 
 
 def load(*paths):
-    """Shapes and their candidates' times; with several runs, the geometric
-    mean of each candidate's times over the runs that timed it in all."""
-    runs = [_last_json(p) for p in paths]
+    """Shapes and their candidates' times; with several runs, per shape the
+    geometric mean of each candidate's times over the runs that timed the
+    shape (candidates every such run timed)."""
+    per_shape = {}
+    for p in paths:
+        for s in _last_json(p)["shapes"]:
+            per_shape.setdefault(tuple(s["shape"]), []).append(s["all"])
     data = []
-    for shapes in zip(*[r["shapes"] for r in runs]):
-        m, n, k = shapes[0]["shape"]
-        assert all(list(s["shape"]) == [m, n, k] for s in shapes), "runs over different shapes"
+    for (m, n, k), runs in per_shape.items():
         times = {}
-        for s in shapes:
-            for name, _est, meas in s["all"]:
+        for cands in runs:
+            for name, _est, meas in cands:
                 times.setdefault(name, []).append(meas)
         cands = []
         for name, ts in times.items():
