@@ -1605,6 +1605,7 @@ int t0_w4a16_gemm(t0_runtime* rt, const t0_w4a16_desc* d) {
     p.zero_const = d->zero_const;
     p.flags = (d->scales_f32 ? T0_W4_SCALE_F32 : 0) | (d->out_f32 ? T0_W4_OUT_F32 : 0);
     p.split_k = pl.split;
+    p.round_wgs = rt->cu_count > 0 ? (uint32_t)rt->cu_count : 256;
     if (!d->zeros && d->zero_const > 15) return fail(T0_ERR_INVALID, "zero_const must be 0..15");
     hipFunction_t f;
     if (pl.kind == 1 && pl.split > 1) {

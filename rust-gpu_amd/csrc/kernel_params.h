@@ -69,7 +69,7 @@ typedef struct t0_w4a16_params {
     uint32_t zero_const;
     uint32_t flags;
     uint32_t split_k;         // decode: K partitions (>= 1)
-    uint32_t pad_;
+    uint32_t round_wgs;       // prefill: workgroups per dispatch round (the CU count)
     // fused residual add + RMSNorm in front of the decode (t0k_w4a16_decode_norm_*,
     // M == 1): the activations are x2 * inv_rms * gamma with x2 = res (+ hid)
     const float* norm_res;    // [K]

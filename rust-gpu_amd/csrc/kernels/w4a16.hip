@@ -505,10 +505,12 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
     // The q-th load of this wave for stage t: its A chunks, its W chunks,
     // then (one wave each) the scales, the zero-point words and the row sums.
     constexpr int NQ = G::A_LOADS + G::W_LOADS + 2;
-    // Workgroups of odd dispatch rounds (256 per round) walk the quant groups
-    // from the last: a CU's next tile shares the previous one's A row band,
-    // whose last groups are then still in the XCD's L2.
-    const bool krev = (bid >> 8) & 1;
+    // Workgroups of odd dispatch rounds (p.round_wgs = the CU count per
+    // round) walk the quant groups from the last: a CU's next tile shares the
+    // previous one's A row band, whose last groups are then still in the
+    // XCD's L2.  Their sum over the groups runs in the reverse order, so a
+    // tile's bits depend on its dispatch round (both within the same bound).
+    const bool krev = p.round_wgs && ((bid / p.round_wgs) & 1);
     auto issue_q = [&](uint32_t t, int q) {
         const uint32_t st = lds_base + __builtin_amdgcn_readfirstlane((t % STAGES) * G::STAGE);
         t = krev ? nk - 1 - t : t;                       // the quant group of step t

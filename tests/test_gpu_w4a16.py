@@ -235,19 +235,23 @@ def test_w4a16_prefill_f32_scales(rt, dev, m, n):
     check_close(got32, ref, w4_tol(a, qw, s, zw, 0, n, k, gs), f"prefill f32 scales {m}x{n}")
 
 
-@pytest.mark.parametrize("per_group_zeros,m,k", [(True, 320, 512), (False, 320, 512),
-                                                 (True, 1024, 128), (True, 1024, 256), (False, 1024, 384),
-                                                 (True, 1024, 1152)])
-def test_w4a16_prefill_exact_integers(rt, dev, per_group_zeros, m, k):
+@pytest.mark.parametrize("per_group_zeros,m,k,n", [(True, 320, 512, 256), (False, 320, 512, 256),
+                                                   (True, 1024, 128, 256), (True, 1024, 256, 256),
+                                                   (False, 1024, 384, 256), (True, 1024, 1152, 256),
+                                                   (True, 4096, 256, 4096), (False, 2048, 640, 8192)])
+def test_w4a16_prefill_exact_integers(rt, dev, per_group_zeros, m, k, n):
     """Integer activations in [-3, 3] and power-of-two scales: every group's
     sum a*(q - z) is an integer below 2^13 and the scaled sum over groups is
     exact in f32, so the f32 output must equal the exact product bit for bit
     (the zero-point term enters as one more MFMA block of row sums).  M = 320
     runs the two-stage 128x128 tiles; M = 1024 the three-stage 128x256 tiles,
     over 1, 2, 3 and 9 quant groups (the peeled last steps alone, and with
-    the loop)."""
+    the loop).  4096x4096 (512 tiles) and 2048x8192 (512 tiles, 5 groups)
+    have more tiles than one dispatch round of one per CU: the tiles of odd
+    rounds walk the quant groups from the last, and with exact sums the order
+    cannot hide a group taken twice or skipped."""
     rng = np.random.default_rng(71 + per_group_zeros + m + k)
-    n, gs = 256, 128
+    gs = 128
     G = k // gs
     qw, _, zw = make_w4(rng, n, k, gs, per_group_zeros=per_group_zeros)
     s = bf16(2.0 ** rng.integers(-8, -4, (G, n)).astype(np.float32))
