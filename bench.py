@@ -248,7 +248,9 @@ def bench_gemm_zero_operands(rt, steps, warmup):
 TILE_SHAPES = [(m, n, k) for m in (32, 128, 512, 1024, 2048, 4096)
                for (n, k) in ((4096, 4096), (11008, 4096), (4096, 11008), (14336, 4096))] + \
               [(4096, 1024, 4096), (3072, 8192, 4096), (384, 4096, 4096), (16, 4096, 4096)] + \
-              [(m, n, 4096) for m in (64, 256) for n in (4096, 11008, 14336)]
+              [(m, n, 4096) for m in (64, 256) for n in (4096, 11008, 14336)] + \
+              [(1, 4096, 4096), (1, 11008, 4096), (1, 4096, 14336), (1, 8192, 28672), (16, 4096, 14336),
+               (128, 4096, 14336), (1024, 4096, 14336), (256, 8192, 28672)]
 
 
 def bench_tiles(rt, steps, warmup, rng, tr):

@@ -4,6 +4,8 @@ kTileCost and the constants beside it) to the measurements that
 candidate timed on LLM shapes (NN, bf16 out, weight operand read cold).
 
     python rust-gpu_amd/t0_gpu/fit_tile_cost.py tiles.json [tiles2.json ...]
+    python rust-gpu_amd/t0_gpu/fit_tile_cost.py --timings profiles/tile_timings.json
+    python rust-gpu_amd/t0_gpu/fit_tile_cost.py --table profiles/tile_timings.json
 
 Several runs are averaged per candidate (geometric mean of the times).
 
@@ -11,8 +13,10 @@ The model is the one rank_candidates evaluates: per workgroup a + b * k_len
 / 1000 us while a round of workgroups (CUs x workgroups per CU, by LDS) is
 resident, a partly filled last round costing DISC + (1 - DISC) * fill of a
 round; co-resident workgroups at most 1 / CO as fast each; no faster than
-A + B + C over HBM, nor the operand re-reads over L2; split-K adding FIX +
-FIX_MB per MB of partial tiles.  Least squares on log time from several
+A + B + C plus the split-K partial tiles (written and read back) over HBM,
+nor the operand re-reads over L2; split-K adding FIX + FIX_MB per MB of
+partial tiles.  (The library's ranking then moves near-ties, within 1 %,
+to the fewest partial bytes and the smallest tile: ``pick``.)  Least squares on log time from several
 starts, then a ranking refinement: per shape, the measured log regret of
 the candidates weighted by a soft minimum of the predicted times (what the
 pick costs), plus W_ERR x the mean squared log error (so the predicted
@@ -59,7 +63,7 @@ def predict(params, t, sk, m, n, k):
     tm = rounds * t_wg
     if slots > CUS:
         tm = max(tm, math.ceil(wgs / CUS) * t_wg * co)
-    hb = k * n * 2.0 + m * k * 2.0 + m * n * 2.0
+    hb = k * n * 2.0 + m * k * 2.0 + m * n * 2.0 + (2.0 * wgs * bm * bn * 4 if sk > 1 else 0.0)
     l2b = m * k * 2.0 * math.ceil(n / bn) + n * k * 2.0 * math.ceil(m / bm)
     tm = max(tm, hb / (hbm * 1e6), l2b / (l2 * 1e6))
     if sk > 1:
@@ -97,6 +101,32 @@ def load(*paths):
     return data
 
 
+CAND = re.compile(r"(\d+)x(\d+)x(\d+)_sk(\d+)_w(\d+)")
+
+
+def load_timings(path, runs=None):
+    """The same from the committed measurements (profiles/tile_timings.json):
+    the runs named (default: the runs the cost table was fitted to)."""
+    with open(path) as f:
+        doc = json.load(f)
+    runs = doc["fit_runs"] if runs is None else runs
+    data = []
+    for s in doc["shapes"]:
+        rs = [r for r in runs if r in s["us"]]
+        if not rs:
+            continue
+        cands = []
+        for i, name in enumerate(s["candidates"]):
+            ts = [s["us"][r][i] for r in rs]
+            if any(t is None for t in ts):
+                continue
+            g = CAND.fullmatch(name)
+            cands.append(((int(g[1]), int(g[2]), int(g[3]), int(g[5])), int(g[4]),
+                          float(np.exp(np.mean(np.log(ts))))))
+        data.append((tuple(s["shape"]), cands))
+    return data
+
+
 def _arrays(data):
     """Per-candidate arrays of the model's inputs (tile index, workgroups,
     rounds structure, bytes) so that a prediction is a few numpy operations."""
@@ -106,7 +136,7 @@ def _arrays(data):
             bm, bn = t[0], t[1]
             slots = CUS * max(1.0, min(math.floor(LDS / lds_bytes(t)), 8.0))
             wgs = math.ceil(m / bm) * math.ceil(n / bn) * sk
-            hb = k * n * 2.0 + m * k * 2.0 + m * n * 2.0
+            hb = k * n * 2.0 + m * k * 2.0 + m * n * 2.0 + (2.0 * wgs * bm * bn * 4 if sk > 1 else 0.0)
             l2b = m * k * 2.0 * math.ceil(n / bn) + n * k * 2.0 * math.ceil(m / bm)
             rows.append((TILES.index(t), wgs / slots, slots > CUS, math.ceil(wgs / CUS), k / sk / 1000.0, hb, l2b,
                          sk > 1, wgs * bm * bn * 4 / 1e6, meas))
@@ -174,17 +204,74 @@ def fit_rank(data, p0):
     return np.clip(r.x, lo, hi)
 
 
+def pick(params, cands, m, n, k):
+    """Index of the candidate the library ranks first: the least predicted
+    time, near-ties (within 1 %) to the fewest partial-tile bytes, then the
+    smallest tile (rank_candidates, csrc/host/config.cpp)."""
+    pr = [predict(params, t, sk, m, n, k) for t, sk, _ in cands]
+    # stable in the library's candidate order: the tile table, then split-K up
+    order = sorted(range(len(cands)), key=lambda i: (pr[i], TILES.index(cands[i][0]), cands[i][1]))
+
+    def part(i):
+        (bm, bn, _, _), sk, _ = cands[i]
+        return math.ceil(m / bm) * math.ceil(n / bn) * sk * bm * bn * 4.0 if sk > 1 else 0.0
+
+    best = order[0]
+    for i in order[1:]:
+        if pr[i] > pr[order[0]] * 1.01:
+            break
+        if part(i) < part(best) or (part(i) == part(best) and
+                                    cands[i][0][0] * cands[i][0][1] < cands[best][0][0] * cands[best][0][1]):
+            best = i
+    return best
+
+
 def regrets(params, data):
     out = []
     for (m, n, k), cands in data:
-        pick = min(range(len(cands)), key=lambda i: predict(params, cands[i][0], cands[i][1], m, n, k))
         best = min(c[2] for c in cands)
-        out.append(cands[pick][2] / best)
+        out.append(cands[pick(params, cands, m, n, k)][2] / best)
     return out
 
 
+def table(path):
+    """Markdown tables of the library's pick (t0_auto_schedule_gemm's rank 0)
+    against the measured best per shape: the fitted runs averaged, then each
+    held-out run."""
+    import os
+    sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    import t0_gpu as t0
+    with open(path) as f:
+        doc = json.load(f)
+    short = lambda t, sk: f"{t[0]}x{t[1]}_k{t[2]}{f'_sk{sk}' if sk > 1 else ''} w{t[3]}"
+    for label, runs in [("fitted runs, averaged", None)] + [(f"held-out run {r}", [r]) for r in doc["held_out_runs"]]:
+        data = load_timings(path, runs)
+        print(f"\n{label}:\n")
+        print("| M x N x K | candidates | pick | pick us | measured best | best us | pick / best | best's predicted rank |")
+        print("|---|---|---|---|---|---|---|---|")
+        reg = []
+        for (m, n, k), cands in data:
+            ranked = t0.auto_schedule_gemm(m, n, k, t0.NN, t0.OUT_BF16)
+            keys = [((c.tile_m, c.tile_n, c.tile_k, c.wg_size // 64), max(c.split_k, 1)) for c, _ in ranked]
+            where = {(t, sk): i for i, (t, sk, _) in enumerate(cands)}
+            ip = where[keys[0]]
+            ib = min(range(len(cands)), key=lambda i: cands[i][2])
+            rank = keys.index((cands[ib][0], cands[ib][1]))
+            reg.append(cands[ip][2] / cands[ib][2])
+            print(f"| {m} x {n} x {k} | {len(cands)} | {short(*cands[ip][:2])} | {cands[ip][2]:.1f} | "
+                  f"{short(*cands[ib][:2])} | {cands[ib][2]:.1f} | {reg[-1]:.3f} | {rank} |")
+        print(f"\npick / best: median {np.median(reg):.3f}, max {max(reg):.3f}, "
+              f"within 3 % on {sum(r <= 1.03 for r in reg)} of {len(reg)}")
+
+
 def main():
-    data = load(*sys.argv[1:])
+    if sys.argv[1:2] == ["--table"]:
+        table(sys.argv[2])
+        return
+    if sys.argv[1:2] == ["--timings"]:
+        data = load_timings(sys.argv[2])
+    else:
+        data = load(*sys.argv[1:])
     params = fit_rank(data, fit(data)[0])
     A = _arrays(data)
     med_err = float(np.median(np.abs(predict_all(params, A) / A["meas"] - 1)))
