@@ -327,8 +327,11 @@ int t0_gemm_clock_probe(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm
  * the call allocates and frees nothing.  Limits: at most
  * T0_NOALLOC_MAX_TILES output tiles and split_k * tiles * tile_m * tile_n * 4
  * <= T0_NOALLOC_SCRATCH_BYTES - 4 * T0_NOALLOC_MAX_TILES bytes of partials,
- * else T0_ERR_INVALID (nothing launched).  The counters used are cleared at
- * each call.  Every call on one GPU shares that GPU's array, so calls that
+ * else T0_ERR_INVALID (nothing launched).  With cfg NULL the call takes
+ * t0_gemm's selection if its split-K fits those limits, else the best-ranked
+ * candidate of t0_auto_schedule_gemm that fits (one without split-K always
+ * does), so its output can then differ from t0_gemm's in rounding (the same
+ * bound).  The counters used are cleared at each call.  Every call on one GPU shares that GPU's array, so calls that
  * overlap on one GPU (other streams, other threads) race. */
 #define T0_NOALLOC_SCRATCH_BYTES (32u << 20)
 #define T0_NOALLOC_MAX_TILES 16384u

@@ -1006,6 +1006,17 @@ int t0_gemm_select(t0_runtime* rt, const t0_gemm_desc* d, t0_gemm_config* out) {
     return T0_OK;
 }
 
+// Whether config c's in-kernel split-K fits the caller's scratch array (its
+// counters and partial tiles, as run_gemm_params lays them out there); a
+// config without split-K needs none.
+static bool scratch_fits(const t0_gemm_config& c, const t0_gemm_desc* d, const Scratch& sc) {
+    const uint32_t sk = split_of(c);
+    if (sk <= 1) return true;
+    const uint64_t tiles = (uint64_t)((d->m + c.tile_m - 1) / c.tile_m) * ((d->n + c.tile_n - 1) / c.tile_n);
+    return tiles <= T0_NOALLOC_MAX_TILES &&
+           sk * tiles * c.tile_m * c.tile_n * 4 <= sc.bytes - (uint64_t)T0_NOALLOC_MAX_TILES * 4;
+}
+
 static int gemm_impl(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm_desc* d, uint64_t* clock_probe,
                      uint32_t* workgroups, const Scratch* sc = nullptr) {
     if (!rt || !d) return fail(T0_ERR_INVALID, "null argument");
@@ -1017,6 +1028,18 @@ static int gemm_impl(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm_de
     else {
         int r = t0_gemm_select(rt, d, &c);
         if (r) return r;
+        if (sc && !scratch_fits(c, d, *sc)) {
+            // the caller's scratch is too small for the selected split: the
+            // best-ranked candidate that fits it, else the selection unsplit
+            t0_gemm_config fit = c;
+            fit.split_k = 0;
+            for (const auto& cand : rank_candidates(d->m, d->n, d->k, d->transpose, d->out_dtype, true))
+                if (scratch_fits(cand.cfg, d, *sc)) {
+                    fit = cand.cfg;
+                    break;
+                }
+            c = fit;
+        }
     }
     const GemmInstance* g = instance_for(c);
     if (!g) return fail(T0_ERR_INFEASIBLE, "%s: no gfx950 kernel", config_name(c).c_str());

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import t0_gpu as t0
-from gpu_util import Dev, bf16
+from gpu_util import Dev, bf16, f32
 
 pytestmark = pytest.mark.gpu
 
@@ -73,5 +73,56 @@ def test_noalloc_refuses_past_its_limits():
                             cfg=big.copy(split_k=0))
             rt.wait_idle()
             assert np.all(d.down(dc, np.uint16, m * n) == 0)
+        finally:
+            d.free()
+
+
+def test_noalloc_without_config_fits_its_scratch():
+    """cfg=None: where the selection's split-K partials exceed the scratch
+    (1024x4096x11008 NN bf16: 256x256 split 4 needs 64 MiB), the call takes
+    the best-ranked candidate that fits, here without split-K; it equals
+    t0_gemm with that config bit for bit, takes no device memory, and
+    agrees with t0_gemm's own selection within the tight bound on sampled
+    rows against float64."""
+    import math
+    from oracle.parity import tight_bound
+    m, n, k = 1024, 4096, 11008
+    scratch, max_tiles = 32 << 20, 16384
+
+    def fits(c):
+        sk = max(c.split_k, 1)
+        tiles = math.ceil(m / c.tile_m) * math.ceil(n / c.tile_n)
+        return sk <= 1 or (tiles <= max_tiles and sk * tiles * c.tile_m * c.tile_n * 4 <= scratch - max_tiles * 4)
+
+    ranked = t0.auto_schedule_gemm(m, n, k, t0.NN, t0.OUT_BF16)
+    assert not fits(ranked[0][0]), ranked[0][0].name()
+    want_cfg = next(c for c, _ in ranked if fits(c))
+    print(f"no-alloc: cfg=None {m}x{n}x{k}, selection {ranked[0][0].name()}, expected {want_cfg.name()}", flush=True)
+    with t0.GpuRuntime(0) as rt:
+        d = Dev(rt)
+        try:
+            rng = np.random.default_rng(31)
+            a = bf16(rng.standard_normal((m, k)))
+            b = bf16(rng.standard_normal((k, n)))
+            da, db = d.up(a), d.up(b)
+            c_na, c_cfg, c_sel = d.zeros(m * n * 2), d.zeros(m * n * 2), d.zeros(m * n * 2)
+            rt.wait_idle()
+            free0 = _free_bytes()
+            rt.gemm_noalloc(da, db, c_na, m, n, k, transpose=t0.NN, out_dtype=t0.OUT_BF16)
+            rt.wait_idle()
+            assert _free_bytes() == free0, "t0_gemm_noalloc took device memory"
+            rt.gemm(da, db, c_cfg, m, n, k, transpose=t0.NN, out_dtype=t0.OUT_BF16,
+                    cfg=want_cfg.copy(transpose=t0.NN, out_dtype=t0.OUT_BF16))
+            rt.gemm(da, db, c_sel, m, n, k, transpose=t0.NN, out_dtype=t0.OUT_BF16)
+            got = d.down(c_na, np.uint16, m * n).reshape(m, n)
+            assert np.array_equal(got, d.down(c_cfg, np.uint16, m * n).reshape(m, n))
+            rows = [0, 1, 511, 1023]
+            af, bf = f32(a[rows]).astype(np.float64), f32(b).astype(np.float64)
+            ref = af @ bf
+            bound = tight_bound(ref, f32(a[rows]), f32(b), True, "nn")
+            sel = d.down(c_sel, np.uint16, m * n).reshape(m, n)
+            for out in (got, sel):
+                err = np.abs(f32(out[rows]).astype(np.float64) - ref)
+                assert np.all(err <= bound), float((err - bound).max())
         finally:
             d.free()
