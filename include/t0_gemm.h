@@ -338,17 +338,25 @@ int t0_gemm_clock_probe(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm
 int t0_gemm_noalloc(t0_runtime* rt, const t0_gemm_config* cfg, const t0_gemm_desc* d);
 
 /* Replaces auto_gemm::GemmTuner::tune (src/t0/auto_gemm.rs:82-216) and the
- * JSON cache (src/t0/auto_gemm.rs:435-501): benchmark candidate configs on
- * the device (hipEvent timing on seeded N(0,1) bf16 operands, median) after a
- * 256^3 correctness smoke test, cache the winner in memory and on disk in the
- * reference's JSON layout (tile_m, tile_n, tile_k, wg_size, split_k, lds_pad,
- * n_col_passes, wgp, swap, tflops, all; plus arch, transpose, out_dtype,
- * name).  NT with f32 output keeps the reference's file name
- * <cache_dir>/gemm_<M>x<N>x<K>.json (reference cache files load); other
- * layouts add _<nn|nt>_<bf16|f32>.  A file is used only if a gfx950 kernel
- * runs its config (tile and wave count, split_k a power of two <= 16) and it
- * names no other architecture; otherwise the candidates are ranked afresh.
- * cfg_out/tflops_out may be NULL. */
+ * JSON cache (src/t0/auto_gemm.rs:435-501): after a 256^3 correctness smoke
+ * test, each of the best-ranked candidate configs is timed on seeded N(0,1)
+ * bf16 operands with the weight operand B rotated through copies that
+ * together exceed the 256 MB Infinity Cache (read from HBM, as in
+ * inference), the launches over all copies captured as one HIP graph and
+ * replayed (hipEvent timing, median of n_iters replays).  The fastest is
+ * cached in memory and on disk in the reference's JSON layout (tile_m,
+ * tile_n, tile_k, wg_size, split_k, lds_pad, n_col_passes, wgp, swap,
+ * tflops, all; plus arch, transpose, out_dtype, name), "all" holding every
+ * timed candidate fastest first as ["name", tflops, wg_size].  NT with f32
+ * output keeps the reference's file name <cache_dir>/gemm_<M>x<N>x<K>.json;
+ * other layouts add _<nn|nt>_<bf16|f32>.  The cache directory is the one
+ * set by t0_tuner_set_cache_dir, else $T0_AUTOTUNE_DIR, else
+ * ~/.t0_autotune_gfx950 (not the reference's ~/.t0_autotune, whose loader
+ * would take gfx950-only configs; set it there to read the reference's
+ * files).  A file is used only if a gfx950 kernel runs its config (tile and
+ * wave count, split_k a power of two <= 16) and it names no other
+ * architecture; otherwise the candidates are ranked afresh.  cfg_out and
+ * tflops_out may be NULL. */
 int t0_tune(t0_runtime* rt, uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype,
             t0_gemm_config* cfg_out, double* tflops_out);
 int t0_tuner_set_cache_dir(const char* dir);
@@ -363,6 +371,19 @@ int t0_tuner_cache_store(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose,
 int t0_tuner_cache_load(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype,
                         t0_gemm_config* cfg, double* tflops);
 int t0_tuner_invalidate(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype);
+/* One timed candidate of t0_tune. */
+typedef struct t0_tune_entry {
+    t0_gemm_config cfg;
+    double tflops;
+} t0_tune_entry;
+/* GemmTuneResult.all (src/t0/auto_gemm.rs:30-42): every candidate the last
+ * t0_tune of this problem timed, fastest first -- from this process's tune
+ * (*from_cache = 0) or else from the cache file's "all" list (*from_cache =
+ * 1; the reference's own loader leaves it empty).  Up to cap entries into
+ * all (may be NULL with cap 0), the count to *n_all; T0_ERR_NOT_FOUND if
+ * neither holds the problem. */
+int t0_tune_results(uint32_t m, uint32_t n, uint32_t k, uint32_t transpose, uint32_t out_dtype, t0_tune_entry* all,
+                    uint32_t cap, uint32_t* n_all, int* from_cache);
 /* Replaces auto_gemm::auto_gemm (src/t0/auto_gemm.rs:555-590): tune then run
  * (NT, f32 out, like the reference). */
 int t0_auto_gemm(t0_runtime* rt, uint64_t a, uint64_t b, uint64_t c, uint32_t m, uint32_t n, uint32_t k,

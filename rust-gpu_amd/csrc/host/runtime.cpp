@@ -264,9 +264,11 @@ uint32_t rd32(const uint8_t* p) { uint32_t v; memcpy(&v, p, 4); return v; }
 float rdf(const uint8_t* p) { float v; memcpy(&v, p, 4); return v; }
 
 // ---------------------------------------------------------------- tuner --
+using TuneList = std::vector<std::pair<t0_gemm_config, double>>;   // (config, TFLOP/s), fastest first
 struct TunerState {
     std::mutex mu;
     std::map<std::string, std::pair<t0_gemm_config, double>> mem;
+    std::map<std::string, TuneList> all;   // every timed candidate of the tunes run in this process
     std::string dir;
     uint32_t max_candidates = 8, n_iters = 10;
 };
@@ -279,8 +281,12 @@ std::string cache_dir() {
     auto& T = tuner();
     if (!T.dir.empty()) return T.dir;
     if (const char* e = getenv("T0_AUTOTUNE_DIR")) return e;
+    // not the reference's ~/.t0_autotune (src/t0/auto_gemm.rs:594-600): its
+    // loader ignores "arch" and would take gfx950-only configs written here;
+    // point the tuner there (t0_tuner_set_cache_dir, T0_AUTOTUNE_DIR) to read
+    // the reference's files
     const char* home = getenv("HOME");
-    return std::string(home ? home : "/tmp") + "/.t0_autotune";   // src/t0/auto_gemm.rs:594-600
+    return std::string(home ? home : "/tmp") + "/.t0_autotune_gfx950";
 }
 
 std::string tune_key_arch(const char* arch, uint32_t m, uint32_t n, uint32_t k, uint32_t tr, uint32_t od) {
@@ -395,8 +401,11 @@ bool load_cache_file(uint32_t m, uint32_t n, uint32_t k, uint32_t tr, uint32_t o
     return true;
 }
 
+// "all" holds every timed candidate, fastest first, as the reference writes
+// it (["name", tflops], src/t0/auto_gemm.rs:480-494) plus a third element,
+// the workgroup size, which the name does not carry.
 bool save_cache_file(uint32_t m, uint32_t n, uint32_t k, uint32_t tr, uint32_t od, const char* arch,
-                     const t0_gemm_config& c, double tf) {
+                     const t0_gemm_config& c, double tf, const TuneList& all) {
     const std::string d = cache_dir();
     mkdir(d.c_str(), 0755);
     std::ofstream f(cache_file(m, n, k, tr, od));
@@ -406,10 +415,47 @@ bool save_cache_file(uint32_t m, uint32_t n, uint32_t k, uint32_t tr, uint32_t o
     f << "{\"tile_m\":" << c.tile_m << ",\"tile_n\":" << c.tile_n << ",\"tile_k\":" << c.tile_k
       << ",\"wg_size\":" << c.wg_size << ",\"split_k\":" << split_of(c) << ",\"lds_pad\":" << c.lds_pad
       << ",\"n_col_passes\":" << (c.n_col_passes ? c.n_col_passes : 1) << ",\"wgp\":" << (c.wgp_mode ? "true" : "false")
-      << ",\"swap\":" << (c.swap_grid ? "true" : "false") << ",\"tflops\":" << num << ",\"all\":[]"
-      << ",\"arch\":\"" << arch << "\",\"transpose\":\"" << (tr == T0_NN ? "nn" : "nt") << "\",\"out_dtype\":\""
+      << ",\"swap\":" << (c.swap_grid ? "true" : "false") << ",\"tflops\":" << num << ",\"all\":[";
+    for (size_t i = 0; i < all.size(); i++) {
+        snprintf(num, sizeof num, "%.2f", all[i].second);
+        f << (i ? "," : "") << "[\"" << config_name(all[i].first) << "\"," << num << "," << all[i].first.wg_size << "]";
+    }
+    f << "],\"arch\":\"" << arch << "\",\"transpose\":\"" << (tr == T0_NN ? "nn" : "nt") << "\",\"out_dtype\":\""
       << (od == T0_OUT_BF16 ? "bf16" : "f32") << "\",\"name\":\"" << config_name(c) << "\"}\n";
     return (bool)f;
+}
+
+// The "all" list of a cache file: entries ["name", tflops] or
+// ["name", tflops, wg_size] whose name parses and runs on gfx950, in file
+// order.  False if the file is missing or names another architecture.
+bool load_cache_all(uint32_t m, uint32_t n, uint32_t k, uint32_t tr, uint32_t od, const char* arch, TuneList* out) {
+    std::string s, a;
+    if (!read_text(cache_file(m, n, k, tr, od), &s)) return false;
+    if (json_raw(s, "arch", &a) && a != arch) return false;
+    out->clear();
+    size_t p = s.find("\"all\":[");
+    if (p == std::string::npos) return true;
+    p += 7;
+    while (p < s.size()) {
+        while (p < s.size() && (s[p] == ' ' || s[p] == ',')) p++;
+        if (p >= s.size() || s[p] != '[') break;
+        const size_t e = s.find(']', p);
+        if (e == std::string::npos) break;
+        const std::string item = s.substr(p + 1, e - p - 1);   // "name",tf[,wg]
+        p = e + 1;
+        const size_t q0 = item.find('"'), q1 = item.find('"', q0 + 1);
+        if (q0 == std::string::npos || q1 == std::string::npos) continue;
+        t0_gemm_config c;
+        if (t0_config_from_name(item.substr(q0 + 1, q1 - q0 - 1).c_str(), &c) != T0_OK) continue;
+        double tf = 0, wg = 0;
+        if (sscanf(item.c_str() + q1 + 1, " ,%lf ,%lf", &tf, &wg) < 1) continue;
+        if (wg > 0) c.wg_size = (uint32_t)wg;
+        c.transpose = (uint8_t)tr;
+        c.out_dtype = (uint8_t)od;
+        if (!tuned_config_ok(c)) continue;
+        out->push_back({c, tf});
+    }
+    return true;
 }
 
 // tile_ir tuning results, tile_ir_MxNxK.json beside the GEMM tuner's files in
@@ -1121,6 +1167,7 @@ int t0_tuner_set_cache_dir(const char* dir) {
     std::lock_guard<std::mutex> g(tuner().mu);
     tuner().dir = dir ? dir : "";
     tuner().mem.clear();
+    tuner().all.clear();
     return T0_OK;
 }
 
@@ -1139,9 +1186,10 @@ int t0_tuner_cache_store(uint32_t m, uint32_t n, uint32_t k, uint32_t tr, uint32
     if (!cfg || !m || !n || !k || tr > T0_NN || od > T0_OUT_BF16) return fail(T0_ERR_INVALID, "bad arguments");
     if (!tuned_config_ok(*cfg)) return fail(T0_ERR_INFEASIBLE, "%s: no gfx950 kernel", config_name(*cfg).c_str());
     std::lock_guard<std::mutex> g(tuner().mu);
-    if (!save_cache_file(m, n, k, tr, od, "gfx950", *cfg, tflops))
+    if (!save_cache_file(m, n, k, tr, od, "gfx950", *cfg, tflops, TuneList{{*cfg, tflops}}))
         return fail(T0_ERR_INVALID, "cannot write %s", cache_file(m, n, k, tr, od).c_str());
     tuner().mem.erase(tune_key_arch("gfx950", m, n, k, tr, od));
+    tuner().all.erase(tune_key_arch("gfx950", m, n, k, tr, od));
     return T0_OK;
 }
 
@@ -1157,7 +1205,30 @@ int t0_tuner_cache_load(uint32_t m, uint32_t n, uint32_t k, uint32_t tr, uint32_
 int t0_tuner_invalidate(uint32_t m, uint32_t n, uint32_t k, uint32_t tr, uint32_t od) {
     std::lock_guard<std::mutex> g(tuner().mu);
     tuner().mem.erase(tune_key_arch("gfx950", m, n, k, tr, od));
+    tuner().all.erase(tune_key_arch("gfx950", m, n, k, tr, od));
     remove(cache_file(m, n, k, tr, od).c_str());
+    return T0_OK;
+}
+
+int t0_tune_results(uint32_t m, uint32_t n, uint32_t k, uint32_t tr, uint32_t od, t0_tune_entry* all, uint32_t cap,
+                    uint32_t* n_all, int* from_cache) {
+    if (!n_all || (cap && !all)) return fail(T0_ERR_INVALID, "null output");
+    if (tr > T0_NN || od > T0_OUT_BF16) return fail(T0_ERR_INVALID, "bad layout / out_dtype");
+    std::lock_guard<std::mutex> g(tuner().mu);
+    TuneList list;
+    int cached = 0;
+    auto it = tuner().all.find(tune_key_arch("gfx950", m, n, k, tr, od));
+    if (it != tuner().all.end()) {
+        list = it->second;
+    } else if (load_cache_all(m, n, k, tr, od, "gfx950", &list)) {
+        cached = 1;
+    } else {
+        return fail(T0_ERR_NOT_FOUND, "%ux%ux%u was not tuned here and %s holds no usable entry", m, n, k,
+                    cache_file(m, n, k, tr, od).c_str());
+    }
+    for (uint32_t i = 0; i < cap && i < list.size(); i++) all[i] = {list[i].first, list[i].second};
+    *n_all = (uint32_t)list.size();
+    if (from_cache) *from_cache = cached;
     return T0_OK;
 }
 
@@ -1249,69 +1320,110 @@ int t0_tune(t0_runtime* rt, uint32_t m, uint32_t n, uint32_t k, uint32_t tr, uin
         if (per_tile[tile]++ >= 2) continue;
         cands.push_back(c.cfg);
     }
-    void *da, *db, *dc;
+    // Operands: seeded N(0,1) values rounded to bf16 (the MFMA clock under
+    // load depends on the data, and constant operands run faster; the
+    // reference zero-fills them, src/t0/auto_gemm.rs:311-314).  The weight
+    // operand B is rotated through copies that together exceed the 256 MB
+    // Infinity Cache, so every launch reads it from HBM as inference does;
+    // the launches over all copies are one HIP graph, replayed and timed.
     const size_t ob = od == T0_OUT_BF16 ? 2 : 4;
-    HIPCHK(hipMalloc(&da, (size_t)m * k * 2));
-    HIPCHK(hipMalloc(&db, (size_t)n * k * 2));
-    HIPCHK(hipMalloc(&dc, (size_t)m * n * ob));
-    {
-        // seeded N(0,1) operands rounded to bf16: the MFMA clock under load
-        // depends on the data (constant operands run faster), so candidates are
-        // timed on data like the callers' (the reference zero-fills them,
-        // src/t0/auto_gemm.rs:311-314)
+    const size_t b_bytes = (size_t)n * k * 2;
+    const uint32_t rot = (uint32_t)std::min<size_t>(64, std::max<size_t>(2, (300ull << 20) / b_bytes + 1));
+    void *da = nullptr, *dc = nullptr;
+    std::vector<void*> db(rot, nullptr);
+    auto free_all = [&]() {
+        hipFree(da);
+        hipFree(dc);
+        for (void* p : db) hipFree(p);
+    };
+    hipError_t he = hipMalloc(&da, (size_t)m * k * 2);
+    if (he == hipSuccess) he = hipMalloc(&dc, (size_t)m * n * ob);
+    for (uint32_t i = 0; i < rot && he == hipSuccess; i++) he = hipMalloc(&db[i], b_bytes);
+    if (he == hipSuccess) {
         std::vector<uint16_t> h(std::max((size_t)m * k, (size_t)n * k));
         fill_normal_bf16(h.data(), (size_t)m * k, 0x9E3779B97F4A7C15ull);
-        HIPCHK(hipMemcpy(da, h.data(), (size_t)m * k * 2, hipMemcpyHostToDevice));
+        he = hipMemcpy(da, h.data(), (size_t)m * k * 2, hipMemcpyHostToDevice);
         fill_normal_bf16(h.data(), (size_t)n * k, 0xD1B54A32D192ED03ull);
-        HIPCHK(hipMemcpy(db, h.data(), (size_t)n * k * 2, hipMemcpyHostToDevice));
+        for (uint32_t i = 0; i < rot && he == hipSuccess; i++) he = hipMemcpy(db[i], h.data(), b_bytes, hipMemcpyHostToDevice);
+    }
+    if (he != hipSuccess) {
+        free_all();
+        return fail(T0_ERR_HIP, "tuner operands (%u copies of B): %s", rot, hipGetErrorString(he));
     }
     t0_gemm_desc d;
     memset(&d, 0, sizeof d);
-    d.a = (uint64_t)da; d.b = (uint64_t)db; d.c = (uint64_t)dc;
+    d.a = (uint64_t)da; d.c = (uint64_t)dc;
     d.m = m; d.n = n; d.k = k;
     d.transpose = tr;
     d.out_dtype = od;
     hipEvent_t e0, e1;
     hipEventCreate(&e0);
     hipEventCreate(&e1);
-    double best_us = 1e30;
-    t0_gemm_config best = cands.empty() ? t0_gemm_config{} : cands[0];
+    TuneList results;
     for (const auto& c : cands) {
         bool ok = false;
         if (smoke_256(rt, c, tr, od, &ok) || !ok) {
             fprintf(stderr, "[autotune] %s -> SKIP (256^3 check failed)\n", config_name(c).c_str());
             continue;
         }
-        if (t0_gemm(rt, &c, &d)) continue;   // warmup
-        std::vector<float> times;
-        for (uint32_t it = 0; it < T.n_iters; it++) {
-            hipEventRecord(e0, rt->stream);
-            if (t0_gemm(rt, &c, &d)) break;
-            hipEventRecord(e1, rt->stream);
-            hipEventSynchronize(e1);
-            float ms = 0;
-            hipEventElapsedTime(&ms, e0, e1);
-            times.push_back(ms);
+        // one eager launch per copy of B: sizes the runtime's workspace
+        // before the capture and warms the code
+        bool bad = false;
+        for (uint32_t i = 0; i < rot && !bad; i++) {
+            d.b = (uint64_t)db[i];
+            bad = t0_gemm(rt, &c, &d) != T0_OK;
         }
+        if (bad || hipStreamSynchronize(rt->stream) != hipSuccess) continue;
+        t0_graph* gr = nullptr;
+        if (t0_graph_begin(rt) != T0_OK) continue;
+        for (uint32_t i = 0; i < rot; i++) {
+            d.b = (uint64_t)db[i];
+            if (t0_gemm(rt, &c, &d) != T0_OK) bad = true;
+        }
+        if (t0_graph_end(rt, &gr) != T0_OK || bad) {
+            t0_graph_destroy(gr);
+            continue;
+        }
+        std::vector<float> times;
+        if (t0_graph_launch(rt, gr) == T0_OK && hipStreamSynchronize(rt->stream) == hipSuccess) {   // warm
+            for (uint32_t it = 0; it < T.n_iters; it++) {
+                hipEventRecord(e0, rt->stream);
+                if (t0_graph_launch(rt, gr) != T0_OK) break;
+                hipEventRecord(e1, rt->stream);
+                hipEventSynchronize(e1);
+                float ms = 0;
+                hipEventElapsedTime(&ms, e0, e1);
+                times.push_back(ms / rot);
+            }
+        }
+        t0_graph_destroy(gr);
         if (times.empty()) continue;
         std::sort(times.begin(), times.end());
         const double us = times[times.size() / 2] * 1e3;
-        if (us < best_us) { best_us = us; best = c; }
+        results.push_back({c, 2.0 * m * n * k / (us * 1e-6) / 1e12});
     }
     hipEventDestroy(e0);
     hipEventDestroy(e1);
-    hipFree(da); hipFree(db); hipFree(dc);
-    if (best_us >= 1e30) {   // src/t0/auto_gemm.rs:125-167: fall back to the static choice
+    hipStreamSynchronize(rt->stream);
+    free_all();
+    std::stable_sort(results.begin(), results.end(),
+                     [](const std::pair<t0_gemm_config, double>& x, const std::pair<t0_gemm_config, double>& y) {
+                         return x.second > y.second;
+                     });
+    t0_gemm_config best;
+    if (results.empty()) {   // src/t0/auto_gemm.rs:125-167: fall back to the static choice
         int rr = t0_auto_select_legacy(m, k, n, &best);
         if (rr) return rr;
         tf = 0;
     } else {
-        tf = 2.0 * m * n * k / (best_us * 1e-6) / 1e12;
-        save_cache_file(m, n, k, tr, od, rt->arch.c_str(), best, tf);
+        best = results[0].first;
+        tf = results[0].second;
+        save_cache_file(m, n, k, tr, od, rt->arch.c_str(), best, tf, results);
     }
     {
         std::lock_guard<std::mutex> g(T.mu);
         T.mem[key] = {best, tf};
+        T.all[key] = results;
     }
     if (cfg_out) *cfg_out = best;
     if (tflops_out) *tflops_out = tf;

@@ -218,6 +218,14 @@ pub const T0_NOALLOC_SCRATCH_BYTES: u32 = 32 << 20;
 /// Most output tiles one `t0_gemm_noalloc` call may have.
 pub const T0_NOALLOC_MAX_TILES: u32 = 16384;
 
+/// One timed candidate of `t0_tune` (GemmTuneResult.all, src/t0/auto_gemm.rs:30-42).
+#[repr(C)]
+#[derive(Clone, Copy, Debug, Default, PartialEq)]
+pub struct t0_tune_entry {
+    pub cfg: t0_gemm_config,
+    pub tflops: f64,
+}
+
 /// One timed candidate of `t0_tile_tune` (TileIrTuneResult, src/t0/cost_model.rs:824-860).
 #[repr(C)]
 #[derive(Clone, Copy, Debug, Default, PartialEq)]
@@ -406,6 +414,8 @@ unsafe extern "C" {
     pub fn t0_tuner_cache_load(m: u32, n: u32, k: u32, transpose: u32, out_dtype: u32, cfg: *mut t0_gemm_config,
                                tflops: *mut f64) -> c_int;
     pub fn t0_tuner_invalidate(m: u32, n: u32, k: u32, transpose: u32, out_dtype: u32) -> c_int;
+    pub fn t0_tune_results(m: u32, n: u32, k: u32, transpose: u32, out_dtype: u32, all: *mut t0_tune_entry, cap: u32,
+                           n_all: *mut u32, from_cache: *mut c_int) -> c_int;
     pub fn t0_auto_gemm(rt: *mut t0_runtime, a: u64, b: u64, c: u64, m: u32, n: u32, k: u32,
                         tflops_out: *mut f64) -> c_int;
     pub fn t0_tile_tune(rt: *mut t0_runtime, m: u32, n: u32, k: u32, best: *mut t0_tile_gemm, best_tflops: *mut f64,

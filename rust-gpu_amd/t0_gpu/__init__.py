@@ -21,7 +21,7 @@ import numpy as np
 
 from . import _ffi
 from ._ffi import (GemmConfigC, GemmDescC, GemmGeometryC, GptqViewC, KernelLoadConfigC, TileGemmC, TileTuneEntryC,
-                   W4A16DescC, lib)
+                   TuneEntryC, W4A16DescC, lib)
 
 NT, NN = 0, 1
 EPI_STORE_F32, EPI_BIAS_ADD, EPI_BIAS_ADD_RELU = 0, 1, 2
@@ -590,6 +590,27 @@ class GemmTuner:
     def invalidate(m: int, n: int, k: int, transpose=NT, out_dtype=OUT_F32):
         """GemmTuner::invalidate (src/t0/auto_gemm.rs:503-507)."""
         _check(lib().t0_tuner_invalidate(m, n, k, transpose, out_dtype))
+
+    @staticmethod
+    def results(m: int, n: int, k: int, transpose=NT, out_dtype=OUT_F32):
+        """GemmTuneResult.all (src/t0/auto_gemm.rs:30-42): every candidate the
+        last tune of this problem timed, fastest first, as (GemmConfig,
+        tflops), and whether the list came from the cache file; None if the
+        problem was never tuned here and has no cache file."""
+        n_all, cached = C.c_uint32(), C.c_int()
+        rc = lib().t0_tune_results(m, n, k, transpose, out_dtype, None, 0, C.byref(n_all), C.byref(cached))
+        if rc == -6:   # T0_ERR_NOT_FOUND
+            return None
+        _check(rc)
+        cap = n_all.value
+        entries = (TuneEntryC * max(cap, 1))()
+        _check(lib().t0_tune_results(m, n, k, transpose, out_dtype, entries, cap, C.byref(n_all), C.byref(cached)))
+        out = []
+        for e in entries[:min(n_all.value, cap)]:
+            c = GemmConfig()
+            C.memmove(C.addressof(c), C.addressof(e.cfg), C.sizeof(GemmConfigC))
+            out.append((c, e.tflops))
+        return out, bool(cached.value)
 
 
 @dataclass

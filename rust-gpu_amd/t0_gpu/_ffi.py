@@ -40,6 +40,10 @@ class TileTuneEntryC(C.Structure):
     _fields_ = [("spec", TileGemmC), ("tflops", C.c_double)]
 
 
+class TuneEntryC(C.Structure):
+    _fields_ = [("cfg", GemmConfigC), ("tflops", C.c_double)]
+
+
 class KernelLoadConfigC(C.Structure):
     _fields_ = [("workgroup_size", u32 * 3), ("lds_size", u32), ("kernarg_size", u32)]
 
@@ -134,6 +138,7 @@ SIGNATURES = {
     "t0_tuner_cache_store": ([u32, u32, u32, u32, u32, P(GemmConfigC), f64], C.c_int),
     "t0_tuner_cache_load": ([u32, u32, u32, u32, u32, P(GemmConfigC), P(f64)], C.c_int),
     "t0_tuner_invalidate": ([u32, u32, u32, u32, u32], C.c_int),
+    "t0_tune_results": ([u32, u32, u32, u32, u32, P(TuneEntryC), u32, P(u32), P(C.c_int)], C.c_int),
     "t0_gemm_noalloc": ([vp, P(GemmConfigC), P(GemmDescC)], C.c_int),
     "t0_gemm_clock_probe": ([vp, P(GemmConfigC), P(GemmDescC), P(f64), P(f64), P(f64)], C.c_int),
     "t0_gemm_select": ([vp, P(GemmDescC), P(GemmConfigC)], C.c_int),

@@ -363,3 +363,55 @@ def test_tuner_cache_reads_reference_files_and_rejects_unusable(tmp_path):
             t0.GemmTuner.save_cache(64, 64, 64, t0.GemmConfig.tile_128x64_k16().copy(wg_size=192), 1.0)
     finally:
         t0.lib().t0_tuner_set_cache_dir(b"")
+
+
+def test_tuner_all_list_on_disk(tmp_path):
+    """GemmTuneResult.all (src/t0/auto_gemm.rs:30-42, written at :480-494):
+    the cache file's "all" list comes back through t0_tune_results, fastest
+    first with each entry's wave count; entries in the reference's two-element
+    form load with the name's instance; entries no gfx950 kernel runs are
+    skipped; another architecture's file, or none, is NOT_FOUND."""
+    t0.lib().t0_tuner_set_cache_dir(str(tmp_path).encode())
+    try:
+        assert t0.GemmTuner.results(512, 512, 512) is None
+        pick = t0.auto_select(4096, 4096, 4096)
+        t0.GemmTuner.save_cache(4096, 4096, 4096, pick, 1234.5)
+        text = (tmp_path / "gemm_4096x4096x4096.json").read_text()
+        assert f'"all":[["{pick.name()}",1234.50,{pick.wg_size}]]' in text, text
+        lst, cached = t0.GemmTuner.results(4096, 4096, 4096)
+        assert cached and len(lst) == 1
+        assert _cfg_fields(lst[0][0]) == _cfg_fields(pick) and lst[0][1] == pytest.approx(1234.5)
+        # a file as a tuning run writes it: several entries, fastest first
+        a = t0.GemmConfig.tile_128x128_k64()
+        b = t0.auto_select(128, 4096, 4096)
+        doc = ('{"tile_m":%d,"tile_n":%d,"tile_k":%d,"wg_size":%d,"split_k":%d,"lds_pad":0,"n_col_passes":1,'
+               '"wgp":false,"swap":true,"tflops":900.00,"all":[["%s",900.00,%d],["%s",800.50],'
+               '["t0_gemm_96x64_k64_ldsdb",700.0,256],["%s",650.0,192]],"arch":"gfx950"}'
+               % (a.tile_m, a.tile_n, a.tile_k, a.wg_size, max(a.split_k, 1), a.name(), a.wg_size, b.name(),
+                  a.name()))
+        (tmp_path / "gemm_2048x2048x2048.json").write_text(doc)
+        lst, cached = t0.GemmTuner.results(2048, 2048, 2048)
+        assert cached
+        assert [(c.name(), c.wg_size, tf) for c, tf in lst] == \
+            [(a.name(), a.wg_size, 900.0), (b.name(), t0.GemmConfig.from_name(b.name()).wg_size, 800.5)]
+        (tmp_path / "gemm_2048x2048x2048.json").write_text(doc.replace('"gfx950"', '"gfx1100"'))
+        assert t0.GemmTuner.results(2048, 2048, 2048) is None
+        t0.GemmTuner.invalidate(4096, 4096, 4096)
+        assert t0.GemmTuner.results(4096, 4096, 4096) is None
+    finally:
+        t0.lib().t0_tuner_set_cache_dir(b"")
+
+
+def test_tuner_default_directory_is_not_the_references(tmp_path, monkeypatch):
+    """Without a directory set, the cache lives in ~/.t0_autotune_gfx950: the
+    reference's loader (src/t0/auto_gemm.rs:439-472) ignores "arch" and would
+    take gfx950-only configs from its own ~/.t0_autotune."""
+    monkeypatch.setenv("HOME", str(tmp_path))
+    monkeypatch.delenv("T0_AUTOTUNE_DIR", raising=False)
+    t0.lib().t0_tuner_set_cache_dir(b"")
+    try:
+        t0.GemmTuner.save_cache(256, 256, 256, t0.auto_select(256, 256, 256), 1.0)
+        assert (tmp_path / ".t0_autotune_gfx950" / "gemm_256x256x256.json").exists()
+        assert not (tmp_path / ".t0_autotune").exists()
+    finally:
+        t0.lib().t0_tuner_set_cache_dir(b"")

@@ -538,10 +538,17 @@ def test_tuner_and_auto_gemm(rt, dev, tmp_path):
     assert f'"wg_size":{cfg.wg_size}' in text and '"arch":"gfx950"' in text, text
     cfg2, tf2 = tuner.tune(rt, 512, 512, 512)
     assert cfg2.name() == cfg.name() and tf2 == tf
+    # GemmTuneResult.all: every timed candidate, fastest first, the pick first
+    timed, cached = tuner.results(512, 512, 512)
+    assert not cached and 1 <= len(timed) <= 4
+    assert [tf_ for _, tf_ in timed] == sorted((tf_ for _, tf_ in timed), reverse=True)
+    assert (timed[0][0].name(), timed[0][0].wg_size, timed[0][1]) == (cfg.name(), cfg.wg_size, tf)
     # a fresh tuner state (as in a new process) reads the same pick back from disk
     tuner3 = t0.GemmTuner(cache_dir=str(tmp_path), max_candidates=4, n_iters=3)
     cfg3, tf3 = tuner3.tune(rt, 512, 512, 512)
     assert (cfg3.name(), cfg3.wg_size) == (cfg.name(), cfg.wg_size) and abs(tf3 - tf) < 0.01
+    timed3, cached3 = tuner3.results(512, 512, 512)
+    assert cached3 and [(c.name(), c.wg_size) for c, _ in timed3] == [(c.name(), c.wg_size) for c, _ in timed]
     m = n = k = 512
     x = orc.xorshift_bf16(m * k, 1).reshape(m, k)
     wt = orc.xorshift_bf16(n * k, 2).reshape(n, k)
