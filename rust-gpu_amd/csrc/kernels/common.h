@@ -33,6 +33,17 @@ T0_DEV void static_for(F&& f) {
 // (>= num_records) read as zero; kernels use OOB_OFFSET to mask lanes.
 constexpr uint32_t OOB_OFFSET = 0x7FFFFFF0u;
 
+// A constant in an SGPR (s_mov_b32), opaque to constant folding: expressions
+// with it select the VOP3 forms that take one scalar operand and no literal
+// (v_and_or_b32 v, v, s, v).  Only the SGPR write is inline asm: the VALU
+// instructions reading it are the compiler's own, so it inserts the wait
+// states an MFMA needs after them.
+T0_DEV uint32_t sgpr_const(uint32_t v) {
+    uint32_t r;
+    asm("s_mov_b32 %0, %1" : "=s"(r) : "i"(v));
+    return r;
+}
+
 T0_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
                                              (int)OOB_OFFSET, 0x00020000);

@@ -85,20 +85,17 @@ T0_DEV void store_out4(const t0_w4a16_params& p, uint32_t m, uint32_t n, f32x4_t
 // 8 nibbles of one u32 (k = 0..7) -> 8 bf16 of value 128 + q, in k order:
 // dword i = bytes (w.byte_i, -, (w >> 4).byte_i, -) masked to the low nibbles
 // and or-ed into 0x4300 (= 128.0).
-// The mask-and-insert is one v_and_or_b32 (the compiler would split it in
-// two: a VOP3 here cannot take the literal, so the constants come in
-// registers, one scalar and one vector).
-T0_DEV uint32_t and_or(uint32_t x, uint32_t mask, uint32_t bits) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(mask), "v"(bits));
-    return r;
-}
-T0_DEV bf16x8_t unpack8_128(uint32_t w, uint32_t bits4300) {
+// The mask-and-insert is one v_and_or_b32: a VOP3 here cannot take a
+// literal, so both constants come in registers, the mask in an SGPR
+// (m000f = sgpr_const(0x000F000F)) and 0x43004300 in a VGPR.  It is plain C,
+// not inline asm: an MFMA that reads a VALU result needs two wait states,
+// which the compiler inserts only after instructions it emitted itself.
+T0_DEV bf16x8_t unpack8_128(uint32_t w, uint32_t bits4300, uint32_t m000f) {
     const uint32_t t = w >> 4;
     u32x4_t r;
 #pragma unroll
     for (int i = 0; i < 4; i++)
-        r[i] = and_or(__builtin_amdgcn_perm(t, w, 0x0C000C00u | ((4u + i) << 16) | (uint32_t)i), 0x000F000Fu, bits4300);
+        r[i] = (__builtin_amdgcn_perm(t, w, 0x0C000C00u | ((4u + i) << 16) | (uint32_t)i) & m000f) | bits4300;
     return __builtin_bit_cast(bf16x8_t, r);
 }
 
@@ -186,6 +183,7 @@ __device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, LDS_AS 
     }
     const float zc_const = 128.0f + (float)p.zero_const;
     const uint32_t bits4300 = __builtin_amdgcn_mov_dpp(0x43004300u, 0xE4, 0xF, 0xF, false);  // in a VGPR
+    const uint32_t m000f = sgpr_const(0x000F000Fu);
     const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, u32x4_t{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
     f32x4_t acc[TILES][MB];
 #pragma unroll
@@ -301,7 +299,7 @@ __device__ __forceinline__ void w4_decode_body(const t0_w4a16_params& p, LDS_AS 
                 }
                 bf16x8_t wv[4];
 #pragma unroll
-                for (int w = 0; w < 4; w++) wv[w] = unpack8_128(wq[s][t][w], bits4300);
+                for (int w = 0; w < 4; w++) wv[w] = unpack8_128(wq[s][t][w], bits4300, m000f);
 #pragma unroll
                 for (int mb = 0; mb < MB; mb++) {
                     f32x4_t tt = {0.f, 0.f, 0.f, 0.f};
@@ -559,6 +557,7 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
     const uint32_t w_sw = ((l32 >> 1) ^ (l32 >> 3)) & 3;
     const uint32_t w_c0 = ((2 * h) ^ w_sw) * 16, w_c1 = ((2 * h + 1) ^ w_sw) * 16;
     const uint32_t bits4300 = __builtin_amdgcn_mov_dpp(0x43004300u, 0xE4, 0xF, 0xF, false);  // in a VGPR
+    const uint32_t m000f = sgpr_const(0x000F000Fu);
 
     // acc += s_n * T for the group whose products are in tmp; sv holds its
     // scales for (j, q4) = columns wn*TN + j*32 + 8*q4 + 4*h .. +3
@@ -688,7 +687,7 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
                 __builtin_amdgcn_sched_barrier(0);
                 bf16x8_t bw[G::FN];
 #pragma unroll
-                for (int j = 0; j < G::FN; j++) bw[j] = unpack8_128(kk < 4 ? wlo[j][kk] : whi[j][kk - 4], bits4300);
+                for (int j = 0; j < G::FN; j++) bw[j] = unpack8_128(kk < 4 ? wlo[j][kk] : whi[j][kk - 4], bits4300, m000f);
 #pragma unroll
                 for (int i = 0; i < G::FM; i++)
 #pragma unroll
@@ -783,7 +782,7 @@ __device__ __forceinline__ void w4_prefill(const t0_w4a16_params& p) {
             }
             bf16x8_t bw[G::FN];
 #pragma unroll
-            for (int j = 0; j < G::FN; j++) bw[j] = unpack8_128(kk < 4 ? wlo[j][kk] : whi[j][kk - 4], bits4300);
+            for (int j = 0; j < G::FN; j++) bw[j] = unpack8_128(kk < 4 ? wlo[j][kk] : whi[j][kk - 4], bits4300, m000f);
 #pragma unroll
             for (int i = 0; i < G::FM; i++)
 #pragma unroll
