@@ -116,3 +116,14 @@ def test_pinned_picks_outside_the_measured_shapes(shape):
     assert pick.name() == PINNED[shape]
     if m == 1:
         assert pick.tile_m == 32
+
+
+@pytest.mark.parametrize("runs,top", [(None, 3), (["c"], 6)])
+def test_measured_best_is_among_the_best_predicted(runs, top):
+    """The tuner times the 8 best-predicted candidates: on every measured
+    shape the measured best is among the first 3 of the library's order on
+    the fitted runs, and the first 6 on the held-out run."""
+    for (m, n, k), cands in F.load_timings(TIMINGS, runs):
+        order = [key(c) for c, _ in t0.auto_schedule_gemm(m, n, k, t0.NN, t0.OUT_BF16)]
+        best = min(cands, key=lambda c: c[2])
+        assert order.index((best[0], best[1])) < top, (m, n, k)
