@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include "../kernel_params.h"
+#include "tile_map.h"
 
 #define T0_DEV __device__ __forceinline__
 #define LDS_AS __attribute__((address_space(3)))
@@ -186,31 +187,6 @@ T0_DEV bool publish_and_count(uint32_t* counter, uint32_t total, uint32_t* lds_f
 T0_DEV void reset_counter(uint32_t* counter) {
     __syncthreads();
     if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// ------------------------------------------------------------- tile order --
-// Workgroups are dispatched round-robin over the 8 XCDs (workgroup b runs on
-// XCD b % 8).  Remap so that consecutive logical ids share an XCD (and its
-// L2): XCD x owns the contiguous id range [start(x), start(x) + count(x)).
-T0_DEV uint32_t xcd_remap(uint32_t b, uint32_t total) {
-    const uint32_t NX = 8;
-    uint32_t x = b % NX, i = b / NX;
-    uint32_t q = total / NX, r = total % NX;
-    uint32_t start = x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q;
-    return start + i;
-}
-
-// Grouped (super-tile) order: GROUP_M tile rows are walked column by column
-// so a run of consecutive ids covers a GROUP_M x (run/GROUP_M) block.
-T0_DEV void grouped_tile(uint32_t id, uint32_t tiles_m, uint32_t tiles_n, uint32_t group_m,
-                         uint32_t& tm, uint32_t& tn) {
-    uint32_t per_group = group_m * tiles_n;
-    uint32_t g = id / per_group;
-    uint32_t first_m = g * group_m;
-    uint32_t gm = min(tiles_m - first_m, group_m);
-    uint32_t in = id - g * per_group;
-    tm = first_m + in % gm;
-    tn = in / gm;
 }
 
 }  // namespace t0

@@ -25,22 +25,6 @@
 
 namespace t0 {
 
-// Swizzle for row-major [rows][CH chunks of 16 B] tiles read 16 lanes x 16 B
-// at a time along rows (A, and B in NT form).
-template <int CH>
-T0_DEV uint32_t swz_rows(uint32_t r) {
-    if constexpr (CH >= 8) return ((r & 7) ^ ((r >> 3) & 1)) & (CH - 1);
-    else if constexpr (CH == 4) return ((r >> 1) ^ (r >> 3)) & 3;
-    else return ((r >> 2) ^ (r >> 3)) & 1;
-}
-
-// Swizzle for the NN B tile [BK][CHB chunks]: the transposed reads take four
-// consecutive k rows x 32 B per 16-lane group.
-template <int CHB>
-T0_DEV uint32_t swz_nn(uint32_t r) {
-    return (0xEA40u >> ((r & 3) * 4)) & 0xFu & (CHB - 1);   // rows 0..3 -> 0, 4, 10, 14
-}
-
 template <int BM, int BN, int BK, int WM, int WN, bool NN, int STAGES>
 struct GemmCfg {
     static constexpr int NW = WM * WN;
