@@ -153,7 +153,7 @@ static uint32_t est_vgprs(const GemmInstance& g) {
     return fm * fn * 16 + (fm + fn) * 8 + 48;
 }
 
-// Per-tile cost, fitted (t0_gpu/fit_tile_cost.py) to every ranked tile x
+// Per-tile cost, fitted (fit_tile_cost.py, beside this file) to every ranked tile x
 // split-K candidate timed on MI355X by `bench.py --only tiles`: 28 LLM
 // shapes (NN, bf16 out, M = 16..4096, N = 1024..14336, K = 4096 or 11008),
 // the weight operand B rotated through more copies than the 256 MB MALL

@@ -3,9 +3,9 @@ kTileCost and the constants beside it) to the measurements that
 ``python bench.py --only tiles`` prints: every ranked tile x split-K
 candidate timed on LLM shapes (NN, bf16 out, weight operand read cold).
 
-    python rust-gpu_amd/t0_gpu/fit_tile_cost.py tiles.json [tiles2.json ...]
-    python rust-gpu_amd/t0_gpu/fit_tile_cost.py --timings profiles/tile_timings.json
-    python rust-gpu_amd/t0_gpu/fit_tile_cost.py --table profiles/tile_timings.json
+    python rust-gpu_amd/csrc/host/fit_tile_cost.py tiles.json [tiles2.json ...]
+    python rust-gpu_amd/csrc/host/fit_tile_cost.py --timings profiles/tile_timings.json
+    python rust-gpu_amd/csrc/host/fit_tile_cost.py --table profiles/tile_timings.json
 
 Several runs are averaged per candidate (geometric mean of the times).
 
@@ -239,7 +239,7 @@ def table(path):
     against the measured best per shape: the fitted runs averaged, then each
     held-out run."""
     import os
-    sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))))
     import t0_gpu as t0
     with open(path) as f:
         doc = json.load(f)

@@ -14,7 +14,7 @@ import pytest
 import t0_gpu as t0
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-sys.path.insert(0, os.path.join(ROOT, "rust-gpu_amd", "t0_gpu"))
+sys.path.insert(0, os.path.join(ROOT, "rust-gpu_amd", "csrc", "host"))
 import fit_tile_cost as F  # noqa: E402
 from test_fit_tile_cost import committed_params  # noqa: E402
 
