@@ -455,7 +455,9 @@ def bench_decode(rt, steps, warmup, rng, tr):
             buf.free()
     a.free()
     dc.free()
-    return {"workload": "W4A16 decode M=16 K=4096 N=11008, g=128, z=8, bf16 out", "kernel": plan[0],
+    return {"workload": "W4A16 decode M=16 K=4096 N=11008, g=128, z=8, bf16 out",
+            "weight_layout": "GPTQ: qweight [N][K/8] u32, 8 nibbles along K; scales [K/128][N] bf16",
+            "kernel": plan[0],
             "split_k": plan[1], "us_per_launch": round(ms * 1e3, 3), "us_median_per_launch": round(med * 1e3, 3),
             "gbs": round(gbs, 1), "bytes_per_launch": bytes_alg, "_host": (a_h, host0[0], host0[1], out0),
             "roofline": roofline("hbm", gbs, PEAK_GBS, "GB/s", traffic_of(tr, "w4a16_decode_16x4096x11008"))}
