@@ -1375,12 +1375,19 @@ int t0_tune(t0_runtime* rt, uint32_t m, uint32_t n, uint32_t k, uint32_t tr, uin
         }
         if (bad || hipStreamSynchronize(rt->stream) != hipSuccess) continue;
         t0_graph* gr = nullptr;
-        if (t0_graph_begin(rt) != T0_OK) continue;
-        for (uint32_t i = 0; i < rot; i++) {
-            d.b = (uint64_t)db[i];
-            if (t0_gemm(rt, &c, &d) != T0_OK) bad = true;
+        int ge;
+        {
+            // the runtime's call lock across the capture: a call from another
+            // thread on this runtime would otherwise land in the graph
+            std::lock_guard<std::recursive_mutex> capture_lock(rt->call_mu);
+            if (t0_graph_begin(rt) != T0_OK) continue;
+            for (uint32_t i = 0; i < rot; i++) {
+                d.b = (uint64_t)db[i];
+                if (t0_gemm(rt, &c, &d) != T0_OK) bad = true;
+            }
+            ge = t0_graph_end(rt, &gr);
         }
-        if (t0_graph_end(rt, &gr) != T0_OK || bad) {
+        if (ge != T0_OK || bad) {
             t0_graph_destroy(gr);
             continue;
         }
